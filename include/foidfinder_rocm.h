@@ -1,0 +1,78 @@
+/* foidfinder_rocm: MI355X (gfx950) kernels for foidfinder's int8 ViT hot path, behind a plain C ABI.
+ *
+ * Every entry point takes raw device pointers, sizes and a hipStream_t passed as void* (NULL = the null stream),
+ * launches asynchronously on that stream, allocates nothing and never synchronizes, so a caller may capture it in a
+ * HIP graph. Buffers are owned by the caller. fp16 tensors are IEEE binary16 passed as void*.
+ *
+ * Return value: FF_OK (0), or a nonzero FF_E* code with a message retrievable through ff_last_error() (thread-local).
+ * Shape and argument preconditions are checked on the host before any HIP call, so they can be exercised without a
+ * GPU. The reference raises RuntimeError through TORCH_CHECK for the same preconditions.
+ */
+#ifndef FOIDFINDER_ROCM_H
+#define FOIDFINDER_ROCM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FF_OK 0
+#define FF_EINVAL 1  /* bad shape / argument */
+#define FF_ELAUNCH 2 /* the HIP runtime rejected a launch */
+
+/* Epilogue codes of ff_gemm_s8. 0-2 keep the reference's values (foidfinder/backends/cuda/csrc/gemm.cuh:8-12). */
+#define FF_EPI_QKV_ROPE 0 /* fp16 out [M,N], N = 3C: RoPE on q and k column pairs (table row m % rope_len), q x q_scale */
+#define FF_EPI_RESIDUAL 1 /* out [M,N] fp16 is the residual stream: out = fp16(fp16(y) + out) */
+#define FF_EPI_GELU_F16 2 /* fp16 out = gelu_tanh(y) */
+#define FF_EPI_SWIGLU 3   /* columns are (gate j, value j) pairs: fp16 out [M, N/2], out[m,j] = silu(y[m,2j]) * y[m,2j+1] */
+#define FF_EPI_BIAS_F16 4 /* fp16 out = y */
+#define FF_EPI_I32 5      /* int32 out [M,N] = the raw accumulators (no scale, no bias) */
+
+/* Version of this ABI; bumps on any signature change. */
+int ff_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* ff_last_error(void);
+
+/* Walsh-Hadamard rotation of fp16 rows of 1024 fused with per-token symmetric int8 quantization.
+ * x fp16 [T,1024] -> out int8 [T,1024], row_scale fp32 [T], value = code * row_scale.
+ * If gamma != NULL, LayerNorm (fp32 gamma/beta [1024], epsilon eps) is applied first.
+ * Replaces op `rot_q8_1024(x, gamma?, beta?, out!, row_scale!)`, foidfinder/backends/cuda/csrc/kernels.cu:220-235
+ * (which fixes eps = 1e-5, kernels.cu:80). */
+int ff_rot_q8_1024(const void* x, const float* gamma, const float* beta, float eps, int64_t T, int8_t* out,
+                   float* row_scale, void* stream);
+
+/* Block-diagonal 128-point Walsh-Hadamard rotation + per-token int8 over rows of C (C % 128 == 0, C <= 6144).
+ * x fp16 [T,C] -> out int8 [T,C], row_scale fp32 [T]. If gamma != NULL, LayerNorm over the first c_real columns
+ * (gamma/beta fp32 [c_real], epsilon eps) is applied first and columns >= c_real are treated as zero padding.
+ * Replaces op `rot_q8_h128(x, out!, row_scale!)`, foidfinder/backends/cuda/csrc/kernels.cu:238-251; the fused norm
+ * is new (EVA02's SwiGLU LayerNorm, foidfinder/backends/mlx/kernels.py:31-72). */
+int ff_rot_q8_h128(const void* x, int64_t T, int64_t C, int64_t c_real, const float* gamma, const float* beta,
+                   float eps, int8_t* out, float* row_scale, void* stream);
+
+/* W8A8 GEMM, exact int32 accumulation, fused epilogue:
+ * y[m,n] = ((float)(sum_k A[m,k] W[n,k]) * row_scale[m]) * col_scale[n] + bias[n], then the epilogue `epi`.
+ * A int8 [M,K], W int8 [N,K] (K contiguous); K % 64 == 0, N % 16 == 0. rope_cos/rope_sin fp32 [rope_len, 32] are
+ * needed by FF_EPI_QKV_ROPE only. `variant` selects the tile shape (0 = default; see ff_gemm_s8_variants).
+ * Replaces op `gemm_s8(A, W, row_scale, col_scale, bias, out!, epi, stages, rope_cos?, rope_sin?, q_scale)`,
+ * foidfinder/backends/cuda/csrc/kernels.cu:187-217, whose `stages` is the same kind of autotuned knob. */
+int ff_gemm_s8(const int8_t* A, const int8_t* W, int64_t M, int64_t N, int64_t K, const float* row_scale,
+               const float* col_scale, const float* bias, void* out, int epi, int variant, const float* rope_cos,
+               const float* rope_sin, int64_t rope_len, float q_scale, void* stream);
+
+/* Number of tile variants ff_gemm_s8 accepts (1 .. n); variant 0 picks the default. */
+int ff_gemm_s8_variants(void);
+
+/* Non-causal flash attention, head_dim 64, over packed qkv rows.
+ * qkv fp16 [T, 3*heads*64] (q already rotated and scaled by softmax_scale*log2(e), k rotated) -> out fp16
+ * [T, heads*64]; T = num_seqs * seq_len; any seq_len >= 1 (tails are masked).
+ * Replaces op `attention(qkv, out!, seq_len)`, foidfinder/backends/cuda/csrc/kernels.cu:255-265 (16 heads and
+ * seq_len % 96 == 0 there). */
+int ff_attention(const void* qkv, void* out, int64_t T, int64_t heads, int64_t seq_len, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

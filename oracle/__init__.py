@@ -1,0 +1,32 @@
+"""CPU oracle for foidfinder's int8 ViT hot path.
+
+TEST INFRASTRUCTURE ONLY. This package restates, in numpy, the arithmetic of the reference's int8 path
+(foidfinder/backends/cuda/csrc/kernels.cu, gemm.cuh, attention.cuh and foidfinder/backends/cuda/engine.py) so the
+HIP kernels can be checked against it on identical inputs. Only `tests/`, `__graft_entry__.smoke()` and the
+`cpu_baseline` leg of `bench.py` may import it, and only as the checker or the timed CPU baseline. The product
+path (`foidfinder_amd`) never imports it and has no CPU fallback.
+
+Modules:
+  rotq8      Walsh-Hadamard rotation + per-token int8 quantization (1024-point and block-128, optional LayerNorm)
+  gemm       exact int8 x int8 -> int32 GEMM and the fp16 epilogues (QKV+RoPE, residual, GELU, SwiGLU, bias)
+  attention  non-causal softmax attention over packed qkv rows, float64
+  model      Hadamard matrix, weight quantization/conversion, EVA02 RoPE tables, synthetic EVA02-L/14-448 weights,
+             and the int8-semantics forward of the whole tagger
+
+Pinning (what checks each function beyond restating it) is listed per function in `PINNED`; tests/test_oracle.py
+runs those checks.
+"""
+
+PINNED = {
+    "model.hadamard": "closed form (-1)^popcount(i&j)/sqrt(n), H H = I, H e0 = 1/sqrt(n)",
+    "model.quantize_rows_int8": "brute-force per-element search of the nearest code on small matrices; ties",
+    "rotq8.fwht_rows": "equals x @ H (float64) to fp32 rounding; stage order only changes rounding (Parseval)",
+    "rotq8.rot_q8_1024": "dequantized codes reconstruct x @ H within half a code; zero row, one-hot row, "
+    "RNE ties; LayerNorm variant vs float64 LayerNorm",
+    "rotq8.rot_q8_h128": "block-diagonal H128 closed form; padded columns stay zero; LN over real columns only",
+    "gemm.gemm_s8_i32": "exact: int64 brute force on small shapes, float64 BLAS bound |acc| < 2^53",
+    "gemm.epilogue": "closed forms: RoPE at cls row is the identity, pair rotation preserves norm, SwiGLU of "
+    "zero-padded columns is zero, residual adds in fp16",
+    "attention.attention": "identical keys -> mean of V; one dominant logit -> that V row; shift invariance",
+    "model.forward_int8": "agrees with the float forward (no quantization) within the int8 error budget",
+}

@@ -1,0 +1,214 @@
+"""Parity of the gfx950 kernels with the CPU oracle on identical seeded inputs, through the C ABI.
+
+Bars: int8 codes, fp32 row scales and int32 accumulators bit-exact; fp16 epilogues without transcendentals
+(bias, residual, QKV+RoPE) bit-exact; GELU/SwiGLU within 1e-3 relative (the GPU's expf/tanhf differ from numpy's by
+an ulp); attention within 4e-3 absolute of the float64 oracle (P is rounded to fp16 before the PV MFMA).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import attention as OA
+from oracle import gemm as OG
+from oracle import model as OM
+from oracle import rotq8 as OR
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def to_gpu(a: np.ndarray, dev) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def activations(rng, T: int, C: int, outlier_frac: float = 0.01) -> np.ndarray:
+    x = rng.standard_normal((T, C), dtype=np.float32)
+    cols = rng.choice(C, max(1, int(C * outlier_frac)), replace=False)
+    x[:, cols] *= 20.0
+    return x.astype(np.float16)
+
+
+def special_rows(C: int) -> np.ndarray:
+    """Zero row, one-hot rows, a constant row, a row of fp16 extremes, an alternating-sign row."""
+    rows = np.zeros((6, C), np.float16)
+    rows[1, 0] = 1.0
+    rows[2, C - 1] = -3.5
+    rows[3, :] = 0.25
+    rows[4, ::3] = 60000.0
+    rows[4, 1::3] = -60000.0
+    rows[5, :] = np.where(np.arange(C) % 2 == 0, 1.0, -1.0)
+    return rows
+
+
+def run_rot1024(x, dev, gamma=None, beta=None, eps=1e-5):
+    from foidfinder_amd import kernels as K
+
+    xt = to_gpu(x, dev)
+    out = torch.empty(x.shape, dtype=torch.int8, device=dev)
+    rs = torch.empty(x.shape[0], dtype=torch.float32, device=dev)
+    g = None if gamma is None else to_gpu(gamma, dev)
+    b = None if beta is None else to_gpu(beta, dev)
+    K.rot_q8_1024(xt, g, b, out, rs, eps)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), rs.cpu().numpy()
+
+
+def assert_codes_equal(got, want, what):
+    (q, s), (q0, s0) = got, want
+    bad = np.flatnonzero((q != q0).any(axis=1) | (s.view(np.uint32) != s0.view(np.uint32)))
+    assert bad.size == 0, f"{what}: {bad.size} rows differ, first {bad[:5]}; scales {s[bad[:3]]} vs {s0[bad[:3]]}"
+
+
+@pytest.mark.parametrize("T", [1, 8, 13, 1025])
+def test_rot_q8_1024_bit_exact(dev, rng, T):
+    x = activations(rng, T, 1024)
+    assert_codes_equal(run_rot1024(x, dev), OR.rot_q8_1024(x), f"rot_q8_1024 T={T}")
+
+
+def test_rot_q8_1024_special_rows(dev):
+    x = special_rows(1024)
+    got = run_rot1024(x, dev)
+    assert_codes_equal(got, OR.rot_q8_1024(x), "special rows")
+    assert (got[0][0] == 0).all() and got[1][0] == np.float32(np.float32(1e-12) / np.float32(127))
+    assert (np.abs(got[0][1].astype(int)) == 127).all()  # one-hot spreads evenly
+
+
+@pytest.mark.parametrize("eps", [1e-5, 1e-6])
+@pytest.mark.parametrize("T", [3, 1025])
+def test_rot_q8_1024_layernorm_bit_exact(dev, rng, T, eps):
+    x = activations(rng, T, 1024)
+    g = (1.0 + 0.02 * rng.standard_normal(1024)).astype(np.float32)
+    b = (0.02 * rng.standard_normal(1024)).astype(np.float32)
+    assert_codes_equal(run_rot1024(x, dev, g, b, eps), OR.rot_q8_1024(x, g, b, eps), f"LN rot T={T}")
+
+
+def run_h128(x, dev, c_real=0, gamma=None, beta=None, eps=1e-6):
+    from foidfinder_amd import kernels as K
+
+    xt = to_gpu(x, dev)
+    out = torch.empty(x.shape, dtype=torch.int8, device=dev)
+    rs = torch.empty(x.shape[0], dtype=torch.float32, device=dev)
+    g = None if gamma is None else to_gpu(gamma, dev)
+    b = None if beta is None else to_gpu(beta, dev)
+    K.rot_q8_h128(xt, out, rs, g, b, c_real, eps)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), rs.cpu().numpy()
+
+
+@pytest.mark.parametrize("C", [128, 640, 768, 2816, 4736])
+@pytest.mark.parametrize("T", [1, 5, 300])
+def test_rot_q8_h128_bit_exact(dev, rng, T, C):
+    x = activations(rng, T, C)
+    assert_codes_equal(run_h128(x, dev), OR.rot_q8_h128(x), f"h128 T={T} C={C}")
+
+
+@pytest.mark.parametrize(("C", "c_real"), [(2816, 2730), (768, 768), (4736, 4736), (256, 130)])
+def test_rot_q8_h128_layernorm_bit_exact(dev, rng, C, c_real):
+    x = activations(rng, 257, C)
+    x[:, c_real:] = 0
+    g = (1.0 + 0.02 * rng.standard_normal(c_real)).astype(np.float32)
+    b = (0.02 * rng.standard_normal(c_real)).astype(np.float32)
+    got = run_h128(x, dev, c_real, g, b, 1e-6)
+    assert_codes_equal(got, OR.rot_q8_h128(x, c_real, g, b, 1e-6), f"LN h128 C={C}")
+
+
+def gemm_inputs(rng, M, N, K):
+    a = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    rs = (rng.random(M, dtype=np.float32) * 0.05 + 1e-3).astype(np.float32)
+    cs = (rng.random(N, dtype=np.float32) * 1e-3 + 1e-5).astype(np.float32)
+    bias = (0.02 * rng.standard_normal(N)).astype(np.float32)
+    return a, w, rs, cs, bias
+
+
+def run_gemm(dev, a, w, rs, cs, bias, epi, variant, out=None, rope=None, q_scale=1.0):
+    from foidfinder_amd import kernels as K
+
+    M, N = a.shape[0], w.shape[0]
+    dtype = torch.int32 if epi == K.EPI_I32 else torch.float16
+    o = torch.empty(K.out_shape(M, N, epi), dtype=dtype, device=dev) if out is None else to_gpu(out, dev)
+    cos, sin = (None, None) if rope is None else (to_gpu(rope[0], dev), to_gpu(rope[1], dev))
+    K.gemm_s8(to_gpu(a, dev), to_gpu(w, dev), to_gpu(rs, dev), to_gpu(cs, dev), to_gpu(bias, dev), o, epi, variant,
+              cos, sin, q_scale)
+    torch.cuda.synchronize()
+    return o.cpu().numpy()
+
+
+GEMM_SHAPES = [(1, 16, 64), (17, 48, 128), (300, 3072, 1024), (1025, 5632, 1024), (129, 1024, 2816), (257, 272, 192)]
+
+
+@pytest.mark.parametrize("variant", [1, 2])
+@pytest.mark.parametrize(("M", "N", "K"), GEMM_SHAPES)
+def test_gemm_s8_int32_bit_exact(dev, rng, M, N, K, variant):
+    a, w, rs, cs, bias = gemm_inputs(rng, M, N, K)
+    got = run_gemm(dev, a, w, rs, cs, bias, OG.EPI_I32, variant)
+    want = OG.gemm_s8_i32(a, w)
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[:4].tolist()}: {got[tuple(bad[0])]} vs {want[tuple(bad[0])]}"
+
+
+@pytest.mark.parametrize("variant", [1, 2])
+@pytest.mark.parametrize("epi", [OG.EPI_BIAS_F16, OG.EPI_RESIDUAL, OG.EPI_QKV_ROPE])
+def test_gemm_s8_epilogue_bit_exact(dev, rng, epi, variant):
+    M, K = 1025, 1024
+    N = 3072 if epi == OG.EPI_QKV_ROPE else 1024
+    a, w, rs, cs, bias = gemm_inputs(rng, M, N, K)
+    kw = {}
+    out = None
+    if epi == OG.EPI_RESIDUAL:
+        out = rng.standard_normal((M, N)).astype(np.float16)
+        kw["residual"] = out
+    rope = None
+    if epi == OG.EPI_QKV_ROPE:
+        rope = OM.eva02_rope_tables(32, 16)
+        kw.update(rope_cos=rope[0], rope_sin=rope[1], q_scale=OM.Q_SCALE)
+    got = run_gemm(dev, a, w, rs, cs, bias, epi, variant, out=out, rope=rope, q_scale=kw.get("q_scale", 1.0))
+    want = OG.gemm_s8(a, w, rs, cs, bias, epi, **kw)
+    bad = np.argwhere(got.view(np.uint16) != want.view(np.uint16))
+    assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[:4].tolist()}: {got[tuple(bad[0])]} vs {want[tuple(bad[0])]}"
+
+
+@pytest.mark.parametrize("epi", [OG.EPI_SWIGLU, OG.EPI_GELU_F16])
+def test_gemm_s8_transcendental_epilogues(dev, rng, epi):
+    M, N, K = 513, 5632, 1024
+    a, w, rs, cs, bias = gemm_inputs(rng, M, N, K)
+    got = run_gemm(dev, a, w, rs, cs, bias, epi, 0).astype(np.float32)
+    want = OG.gemm_s8(a, w, rs, cs, bias, epi).astype(np.float32)
+    np.testing.assert_allclose(got, want, rtol=1e-3, atol=1e-4)
+
+
+def run_attention(dev, qkv, seq_len):
+    from foidfinder_amd import kernels as K
+
+    t = to_gpu(qkv, dev)
+    out = torch.empty(qkv.shape[0], qkv.shape[1] // 3, dtype=torch.float16, device=dev)
+    K.attention(t, out, seq_len)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def qkv_inputs(rng, S, L, H):
+    x = rng.standard_normal((S * L, 3 * H * 64), dtype=np.float32)
+    x[:, : H * 64] *= np.float32(OM.Q_SCALE)
+    return x.astype(np.float16)
+
+
+@pytest.mark.parametrize(("S", "L", "H"), [(1, 1, 16), (2, 65, 16), (1, 1025, 16), (2, 1025, 12), (1, 577, 16), (3, 128, 2)])
+def test_attention_matches_float64(dev, rng, S, L, H):
+    qkv = qkv_inputs(rng, S, L, H)
+    got = run_attention(dev, qkv, L).astype(np.float64)
+    want = OA.attention(qkv, L, out_dtype=np.float64)
+    err = np.abs(got - want).max()
+    assert np.isfinite(got).all() and err < 4e-3, f"max abs err {err}"
+
+
+def test_attention_identical_keys_give_mean_of_values(dev, rng):
+    S, L, H = 1, 200, 4
+    qkv = qkv_inputs(rng, S, L, H)
+    qkv[:, H * 64 : 2 * H * 64] = qkv[0, H * 64 : 2 * H * 64]  # every key equal
+    got = run_attention(dev, qkv, L).astype(np.float64)
+    v = qkv[:, 2 * H * 64 :].astype(np.float64)
+    np.testing.assert_allclose(got, np.broadcast_to(v.mean(0), got.shape), atol=2e-3)
