@@ -1,0 +1,213 @@
+"""Throughput of the int8 EVA02-L/14-448 tagger forward on one MI355X, batch 32, HIP-graph replay.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--batch 32] [--no-cpu-baseline]
+
+A step is one forward over a batch of synthetic images (uniform [-1, 1], NHWC fp16, already in HBM) through the
+captured graph: patch-embed GEMM, 24 int8 blocks (3x rotate+quant 1024, rotate+quant h128 + LayerNorm, 4 int8 GEMMs
+with fused epilogues, flash attention), final LayerNorm, 1024 -> 30877 tag GEMM. Weights are random-init (seeded).
+
+Prints one JSON line: images/s (whole job), per-kernel times measured live with HIP events on the launch stream,
+the roofline of the dominant kernel, and the CPU baseline (the numpy oracle's int8 forward on a bounded sample).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA, TOP/s
+PEAK_FP16_TFLOPS = 2500.0  # dense fp16 MFMA
+PEAK_HBM_GBS = 8000.0
+METRIC = "images/sec @448px int8 ViT-L batch 32; int8 GEMM TOPS and % of MFMA peak"
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--batch", type=int, default=32)
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-images", type=int, default=1, help="images in the CPU baseline sample")
+    return p.parse_args()
+
+
+def timed(fn, stream, iters=20, warm=3) -> float:
+    """Average duration (us) of fn's launches, HIP events recorded on the stream the kernels run on."""
+    import torch
+
+    for _ in range(warm):
+        fn()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record(stream)
+    for _ in range(iters):
+        fn()
+    e.record(stream)
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / iters * 1e3
+
+
+def kernel_table(eng, B: int, buf) -> dict:
+    """Each block kernel timed in isolation on the graph's buffers; algorithmic work per launch and roofline."""
+    import torch
+
+    from foidfinder_amd.kernels import EPI_QKV_ROPE, EPI_RESIDUAL, EPI_SWIGLU
+
+    cfg, k, lw = eng.cfg, eng.k, eng.layers[0]
+    M, d, h, hp = B * cfg.tokens, cfg.dim, cfg.hidden, cfg.hidden_pad
+    st = torch.cuda.current_stream()
+    v = {n: eng.variants.get((n, B), 0) for n in ("qkv", "proj", "fc1", "fc2")}
+    x2 = buf["x"].clone()  # residual epilogues write into a scratch copy
+    jobs = {
+        "rot_q8_1024_ln": (lambda: k.rot_q8_1024(buf["x"], *lw["n1"], buf["a8"], buf["rs"], cfg.eps),
+                           "hbm", M * d * 2 + M * d + 4 * M + 8 * d, 2 * cfg.depth),
+        "rot_q8_1024": (lambda: k.rot_q8_1024(buf["o16"], None, None, buf["a8"], buf["rs"], cfg.eps),
+                        "hbm", M * d * 3 + 4 * M, cfg.depth),
+        "rot_q8_h128_ln": (lambda: k.rot_q8_h128(buf["h16"], buf["h8"], buf["rs"], *lw["nm"], h, cfg.eps),
+                           "hbm", M * hp * 3 + 4 * M + 8 * h, cfg.depth),
+        "gemm_qkv": (lambda: eng._gemm(buf["a8"], lw["qkv"], buf["rs"], EPI_QKV_ROPE, v["qkv"], buf["qkv"], eng.rope),
+                     "mfma_int8", 2 * M * 3 * d * d, cfg.depth),
+        "gemm_proj": (lambda: eng._gemm(buf["a8"], lw["proj"], buf["rs"], EPI_RESIDUAL, v["proj"], x2),
+                      "mfma_int8", 2 * M * d * d, cfg.depth),
+        "gemm_fc1": (lambda: eng._gemm(buf["a8"], lw["fc1"], buf["rs"], EPI_SWIGLU, v["fc1"], buf["h16"]),
+                     "mfma_int8", 2 * M * 2 * h * d, cfg.depth),
+        "gemm_fc2": (lambda: eng._gemm(buf["h8"], lw["fc2"], buf["rs"], EPI_RESIDUAL, v["fc2"], x2),
+                     "mfma_int8", 2 * M * d * h, cfg.depth),
+        "attention": (lambda: k.attention(buf["qkv"], buf["o16"], cfg.tokens),
+                      "mfma_fp16", 4 * B * cfg.heads * cfg.tokens * cfg.tokens * 64, cfg.depth),
+    }
+    out = {}
+    for name, (fn, bound, work, per_fwd) in jobs.items():
+        us = timed(fn, st)
+        if bound == "hbm":
+            ach, peak, unit = work / us / 1e3, PEAK_HBM_GBS, "GB/s"
+        elif bound == "mfma_int8":
+            ach, peak, unit = work / us / 1e6, PEAK_INT8_TOPS, "TFLOP/s"
+        else:
+            ach, peak, unit = work / us / 1e6, PEAK_FP16_TFLOPS, "TFLOP/s"
+        out[name] = {"us": round(us, 2), "launches_per_step": per_fwd, "work_per_launch": work,
+                     "achieved": round(ach, 1), "unit": unit, "peak": peak, "frac": round(ach / peak, 4),
+                     "bound": "hbm" if bound == "hbm" else "mfma"}
+    return out
+
+
+def cpu_baseline(state, cfg, n_images: int) -> dict:
+    """The numpy oracle's int8-semantics forward (a port of the reference's int8 path) on n_images images."""
+    import numpy as np
+
+    from oracle import model as OM
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
+    except Exception:  # noqa: BLE001
+        threads = os.cpu_count() or 1
+    np_state = {k: v.detach().cpu().numpy() for k, v in state.items()}
+    ocfg = OM.Eva02Config(img_size=cfg.img_size, depth=cfg.depth, tags=cfg.tags)
+    images = OM.synthetic_images(n_images, cfg.img_size, seed=11)
+    t = time.perf_counter()
+    OM.forward_int8_state(images, np_state, ocfg)
+    dt = time.perf_counter() - t
+    return {"value": round(n_images / dt, 4), "unit": "images/s", "cores": threads, "kind": "port",
+            "sample": f"{n_images} image(s) through the full 24-block EVA02-L/14-448 int8 forward "
+                      f"(numpy oracle, float64 BLAS for the exact int32 GEMMs), {dt:.1f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}): the tagger forward is data-parallel "
+              "over images and every figure here is one GPU's", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from foidfinder_amd.engine import Eva02Config, Eva02Int8, convert_checkpoint, synthetic_checkpoint
+
+    torch.manual_seed(args.seed)
+    dev = torch.device("cuda:0")
+    cfg = Eva02Config()
+    B = args.batch
+    t0 = time.perf_counter()
+    raw = synthetic_checkpoint(cfg, seed=args.seed)
+    state = convert_checkpoint({k: v.to(dev) for k, v in raw.items()}, cfg)
+    del raw
+    eng = Eva02Int8(state, cfg, device=dev)
+    g = torch.Generator(device="cpu").manual_seed(args.seed + 1)
+    images = (torch.rand(B, cfg.img_size, cfg.img_size, 3, generator=g) * 2 - 1).half().to(dev)
+    logits = eng(images)  # autotune + capture
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t0
+    print(f"setup {setup_s:.1f}s (weights, conversion, autotune, graph capture); variants "
+          f"{ {k[0]: v for k, v in eng.variants.items()} }", file=sys.stderr, flush=True)
+    assert torch.isfinite(logits).all()
+
+    for _ in range(args.warmup):
+        eng.replay(B)
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(args.steps):
+        eng.replay(B)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    ms = elapsed / args.steps * 1e3
+    ips = B * args.steps / elapsed
+    print(f"{ips:.1f} images/s, {ms:.2f} ms per batch of {B}", file=sys.stderr, flush=True)
+
+    buf = eng._graphs[B][3]
+    kern = kernel_table(eng, B, buf)
+    per_step = {n: r["us"] * r["launches_per_step"] for n, r in kern.items()}
+    dom = max(per_step, key=per_step.get)
+    dk = kern[dom]
+    traffic = None
+    tf = ROOT / "profiles" / "traffic.json"
+    if tf.exists():
+        traffic = json.loads(tf.read_text()).get(dom)
+    gemm_names = [n for n in kern if n.startswith("gemm_")]
+    gemm_ops = sum(kern[n]["work_per_launch"] * kern[n]["launches_per_step"] for n in gemm_names)
+    gemm_us = sum(per_step[n] for n in gemm_names)
+    gemm_tops = gemm_ops / gemm_us / 1e6
+    for n, r in kern.items():
+        print(f"  {n:16s} {r['us']:8.1f} us x{r['launches_per_step']:3d}  {r['achieved']:8.1f} {r['unit']}"
+              f"  ({100 * r['frac']:.1f}% of peak)", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(state, cfg, args.cpu_images)
+    line = {
+        "metric": METRIC,
+        "value": round(ips, 2),
+        "unit": "images/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic: random-init weights (seeded), images uniform [-1, 1]",
+        "config": {"workload": "EVA02-L/14-448 int8 W8A8 tagger forward, batch 32, hipGraph replay",
+                   "batch": B, "seq_len": cfg.tokens, "dim": cfg.dim, "depth": cfg.depth, "heads": cfg.heads,
+                   "mlp_hidden": cfg.hidden, "tags": cfg.tags, "parallelism": "single GPU"},
+        "gemm_tops": round(gemm_tops, 1),
+        "gemm_frac_of_int8_peak": round(gemm_tops / PEAK_INT8_TOPS, 4),
+        "roofline": {"kernel": dom, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
+                     "unit": dk["unit"], "frac": dk["frac"], "traffic": traffic},
+        "kernels": kern,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

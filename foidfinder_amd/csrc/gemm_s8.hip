@@ -44,7 +44,25 @@ __device__ __forceinline__ int xcd_remap(int b, int nblocks) {
   return x * q + (x < r ? x : r) + k;
 }
 
-__device__ __forceinline__ float silu(float g) { return g / (1.f + expf(-g)); }
+// exp(x) from plain fp32 operations in a fixed order (no fused multiply-add: this file is built with
+// -ffp-contract=off), so the CPU oracle reproduces it bit for bit: Cody-Waite range reduction x = n ln2 + r with ln2
+// split into a 16-bit head and a tail (n * head is exact for |n| < 256), a degree-6 Taylor polynomial for e^r on
+// |r| <= ln2/2, then an exact scaling by 2^n; relative error below 3e-7 over [-80, 80].
+__device__ __forceinline__ float exp_cw(float x) {
+  const float n = __builtin_rintf(x * 1.44269504088896341f);
+  const float r = (x - n * 0.693145751953125f) - n * 1.428606765330187045e-06f;
+  float p = 1.f / 720.f;
+  p = p * r + 1.f / 120.f;
+  p = p * r + 1.f / 24.f;
+  p = p * r + 1.f / 6.f;
+  p = p * r + 0.5f;
+  p = p * r + 1.f;
+  p = p * r + 1.f;
+  const int e = static_cast<int>(fminf(fmaxf(n, -300.f), 300.f));
+  return ldexpf(p, e);
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.f + exp_cw(-g)); }
 
 __device__ __forceinline__ float gelu_tanh(float y) {
   return 0.5f * y * (1.f + tanhf(0.7978845608f * (y + 0.044715f * y * y * y)));

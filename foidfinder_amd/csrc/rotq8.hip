@@ -165,15 +165,20 @@ __global__ __launch_bounds__(256) void rot_q8_h128_kernel(const half_t* __restri
     }
   }
   if constexpr (NORM) {
-    // LayerNorm over the first c_real columns; the rest are padding and stay zero.
+    // LayerNorm over the first c_real columns; the rest are padding and stay zero. nreal[i] = how many of the
+    // lane's 8 columns of block 4i + g are real (the prefix e < nreal[i]).
+    int nreal[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int b = 4 * i + g;
+      const int left = c_real - (b * 128 + 8 * s);
+      nreal[i] = b < nb ? (left < 0 ? 0 : (left > 8 ? 8 : left)) : 0;
+    }
     float sum = 0.f;
 #pragma unroll
     for (int i = 0; i < NI; ++i)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int col = (4 * i + g) * 128 + 8 * s + e;
-        sum = sum + ((4 * i + g) < nb && col < c_real ? v[i * 8 + e] : 0.f);
-      }
+      for (int e = 0; e < 8; ++e) sum = sum + (e < nreal[i] ? v[i * 8 + e] : 0.f);
     const float fr = static_cast<float>(c_real);
     const float mean = wave_sum(sum) / fr;
     float sq = 0.f;
@@ -181,24 +186,42 @@ __global__ __launch_bounds__(256) void rot_q8_h128_kernel(const half_t* __restri
     for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int col = (4 * i + g) * 128 + 8 * s + e;
-        const bool real = (4 * i + g) < nb && col < c_real;
-        const float d = real ? v[i * 8 + e] - mean : 0.f;
+        const float d = e < nreal[i] ? v[i * 8 + e] - mean : 0.f;
         v[i * 8 + e] = d;
         sq = sq + d * d;
       }
     const float var = wave_sum(sq) / fr;
     const float rstd = 1.f / sqrtf(var + eps);
 #pragma unroll
-    for (int i = 0; i < NI; ++i)
+    for (int i = 0; i < NI; ++i) {
+      const int col0 = (4 * i + g) * 128 + 8 * s;
+      float gg[8], bb[8];
+      if (nreal[i] == 8) {
+        const float4_t g0 = *reinterpret_cast<const float4_t*>(gamma + col0);
+        const float4_t g1 = *reinterpret_cast<const float4_t*>(gamma + col0 + 4);
+        const float4_t b0 = *reinterpret_cast<const float4_t*>(beta + col0);
+        const float4_t b1 = *reinterpret_cast<const float4_t*>(beta + col0 + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          gg[e] = g0[e];
+          gg[e + 4] = g1[e];
+          bb[e] = b0[e];
+          bb[e + 4] = b1[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int cc = e < nreal[i] ? col0 + e : 0;  // never read gamma/beta past c_real
+          gg[e] = gamma[cc];
+          bb[e] = beta[cc];
+        }
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int col = (4 * i + g) * 128 + 8 * s + e;
-        const bool real = (4 * i + g) < nb && col < c_real;
-        const int cc = real ? col : 0;  // never read gamma/beta past c_real
-        const float y = v[i * 8 + e] * rstd * gamma[cc] + beta[cc];
-        v[i * 8 + e] = real ? y : 0.f;
+        const float y = v[i * 8 + e] * rstd * gg[e] + bb[e];
+        v[i * 8 + e] = e < nreal[i] ? y : 0.f;
       }
+    }
   }
   // column bits 0, 1, 2 (registers)
 #pragma unroll
@@ -289,7 +312,7 @@ extern "C" int ff_rot_q8_h128(const void* x, int64_t T, int64_t C, int64_t c_rea
   if (gamma && !(eps > 0.f)) return fail(FF_EINVAL, "rot_q8_h128: eps must be > 0");
   if (T == 0) return FF_OK;
   if (!x || !out || !row_scale) return fail(FF_EINVAL, "rot_q8_h128: null pointer");
-  if (!aligned(x, 16) || !aligned(out, 8) || !aligned(row_scale, 4))
+  if (!aligned(x, 16) || !aligned(out, 8) || !aligned(row_scale, 4) || (gamma && (!aligned(gamma, 16) || !aligned(beta, 16))))
     return fail(FF_EINVAL, "rot_q8_h128: misaligned pointer");
   const int64_t blocks = (T + 3) / 4;
   if (blocks > 0x7fffffff) return fail(FF_EINVAL, "rot_q8_h128: T too large");

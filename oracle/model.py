@@ -69,12 +69,12 @@ def eva02_rope_tables(grid: int, ref: int, head_dim: int = 64) -> tuple[np.ndarr
     interleaved (even, odd) pair; row 0 (cls) is the identity. Angles: pairs 0..15 use the row (y) position, pairs
     16..31 the column (x) position, positions rescaled to the pretraining grid (foidfinder/backends/mlx/haruka.py:22-33)."""
     q = head_dim // 4
-    bands = F32(1.0) / (F32(10000.0) ** (np.arange(q, dtype=F32) / F32(q)))
-    t = np.arange(grid, dtype=F32) / F32(grid) * F32(ref)
+    bands = 1.0 / (10000.0 ** (np.arange(q, dtype=np.float64) / q))
+    t = np.arange(grid, dtype=np.float64) / grid * ref
     ty, tx = np.meshgrid(t, t, indexing="ij")
-    ang = np.concatenate([ty.reshape(-1, 1) * bands, tx.reshape(-1, 1) * bands], axis=1).astype(F32)
-    cos = np.concatenate([np.ones((1, head_dim // 2), F32), np.cos(ang)])
-    sin = np.concatenate([np.zeros((1, head_dim // 2), F32), np.sin(ang)])
+    ang = np.concatenate([ty.reshape(-1, 1) * bands, tx.reshape(-1, 1) * bands], axis=1)  # float64, rounded once
+    cos = np.concatenate([np.ones((1, head_dim // 2)), np.cos(ang)]).astype(F32)
+    sin = np.concatenate([np.zeros((1, head_dim // 2)), np.sin(ang)]).astype(F32)
     return np.ascontiguousarray(cos), np.ascontiguousarray(sin)
 
 
@@ -241,15 +241,28 @@ def head(x: np.ndarray, w: FloatWeights) -> np.ndarray:
     return (1.0 / (1.0 + np.exp(-logits))).astype(F32)
 
 
-def block_int8(x: np.ndarray, qb: dict[str, np.ndarray], cfg: Eva02Config, rope: tuple[np.ndarray, np.ndarray]):
-    """One int8 block on the fp16 residual stream x [B*L, d] -> new x."""
+def block_int8(
+    x: np.ndarray,
+    qb: dict[str, np.ndarray],
+    cfg: Eva02Config,
+    rope: tuple[np.ndarray, np.ndarray],
+    *,
+    attention_out: np.ndarray | None = None,
+    record: dict | None = None,
+):
+    """One int8 block on the fp16 residual stream x [B*L, d] -> new x.
+
+    attention_out, if given, replaces the attention output (teacher forcing: every other op is then a pure function
+    of its inputs, so a kernel implementation must reproduce the block bit for bit); record collects qkv and o."""
     cos, sin = rope
     a8, rs = rotq8.rot_q8_1024(x, qb["norm1_w"], qb["norm1_b"], cfg.eps)
     qkv = G.gemm_s8(
         a8, qb["qkv.qweight"], rs, qb["qkv.wscale"], qb["qkv.bias"], G.EPI_QKV_ROPE,
         rope_cos=cos, rope_sin=sin, q_scale=Q_SCALE,
     )
-    o = attn_mod.attention(qkv, cfg.tokens)
+    o = attn_mod.attention(qkv, cfg.tokens) if attention_out is None else attention_out
+    if record is not None:
+        record["qkv"], record["o"] = qkv, o
     a8, rs = rotq8.rot_q8_1024(o)
     x = G.gemm_s8(a8, qb["proj.qweight"], rs, qb["proj.wscale"], qb["proj.bias"], G.EPI_RESIDUAL, residual=x)
     a8, rs = rotq8.rot_q8_1024(x, qb["norm2_w"], qb["norm2_b"], cfg.eps)
@@ -319,3 +332,39 @@ def w8a8_linear_inputs(m: int = 1025, k: int = 1024, n: int = 3072, seed: int = 
     ws = ws.astype(np.float16).astype(F32)
     bias = rng.standard_normal(n, dtype=F32) * F32(0.02)
     return x.astype(np.float16), qw, ws, bias.astype(F32)
+
+
+def blocks_from_state(state: dict[str, np.ndarray], depth: int) -> list[dict[str, np.ndarray]]:
+    """Engine-format state dict (keys `blocks.{i}.attn.qkv.qweight`, ...) -> the per-block dicts block_int8 takes."""
+    names = {"qkv": "attn.qkv", "proj": "attn.proj", "fc1": "mlp.fc1", "fc2": "mlp.fc2"}
+    out = []
+    for i in range(depth):
+        p = f"blocks.{i}."
+        qb = {}
+        for short, long in names.items():
+            for f in ("qweight", "wscale", "bias"):
+                qb[f"{short}.{f}"] = state[p + long + "." + f]
+        for short, long in (("norm1", "norm1"), ("norm2", "norm2"), ("mlp_norm", "mlp.norm")):
+            qb[short + "_w"] = state[p + long + ".weight"].astype(F32)
+            qb[short + "_b"] = state[p + long + ".bias"].astype(F32)
+        out.append(qb)
+    return out
+
+
+def float_weights_from_state(state: dict[str, np.ndarray], cfg: Eva02Config) -> FloatWeights:
+    """The non-block tensors of an engine-format state dict as FloatWeights (stem and head)."""
+    w = FloatWeights(
+        cfg=cfg,
+        patch_w=state["patch_embed.weight"].astype(F32),
+        patch_b=state["patch_embed.bias"].astype(F32),
+        cls=state["cls_token"].astype(F32).reshape(cfg.dim),
+        pos=state["pos_embed"].astype(F32).reshape(cfg.tokens, cfg.dim),
+    )
+    w.norm_w, w.norm_b = state["norm.weight"].astype(F32), state["norm.bias"].astype(F32)
+    w.head_w, w.head_b = state["head.weight"].astype(F32), state["head.bias"].astype(F32)
+    return w
+
+
+def forward_int8_state(images: np.ndarray, state: dict[str, np.ndarray], cfg: Eva02Config) -> np.ndarray:
+    """forward_int8 driven by an engine-format state dict."""
+    return forward_int8(images, float_weights_from_state(state, cfg), blocks_from_state(state, cfg.depth))

@@ -1,8 +1,8 @@
 """Parity of the gfx950 kernels with the CPU oracle on identical seeded inputs, through the C ABI.
 
-Bars: int8 codes, fp32 row scales and int32 accumulators bit-exact; fp16 epilogues without transcendentals
-(bias, residual, QKV+RoPE) bit-exact; GELU/SwiGLU within 1e-3 relative (the GPU's expf/tanhf differ from numpy's by
-an ulp); attention within 4e-3 absolute of the float64 oracle (P is rounded to fp16 before the PV MFMA).
+Bars: int8 codes, fp32 row scales and int32 accumulators bit-exact; fp16 epilogues bias, residual, QKV+RoPE and
+SwiGLU (its exp is a fixed sequence of fp32 operations) bit-exact; GELU within 1e-3 relative (the GPU's tanhf differs
+from numpy's by an ulp); attention within 4e-3 absolute of the float64 oracle (P is rounded to fp16 before the PV MFMA).
 """
 
 from __future__ import annotations
@@ -151,10 +151,10 @@ def test_gemm_s8_int32_bit_exact(dev, rng, M, N, K, variant):
 
 
 @pytest.mark.parametrize("variant", [1, 2])
-@pytest.mark.parametrize("epi", [OG.EPI_BIAS_F16, OG.EPI_RESIDUAL, OG.EPI_QKV_ROPE])
+@pytest.mark.parametrize("epi", [OG.EPI_BIAS_F16, OG.EPI_RESIDUAL, OG.EPI_QKV_ROPE, OG.EPI_SWIGLU])
 def test_gemm_s8_epilogue_bit_exact(dev, rng, epi, variant):
     M, K = 1025, 1024
-    N = 3072 if epi == OG.EPI_QKV_ROPE else 1024
+    N = {OG.EPI_QKV_ROPE: 3072, OG.EPI_SWIGLU: 5632}.get(epi, 1024)
     a, w, rs, cs, bias = gemm_inputs(rng, M, N, K)
     kw = {}
     out = None
@@ -171,12 +171,11 @@ def test_gemm_s8_epilogue_bit_exact(dev, rng, epi, variant):
     assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[:4].tolist()}: {got[tuple(bad[0])]} vs {want[tuple(bad[0])]}"
 
 
-@pytest.mark.parametrize("epi", [OG.EPI_SWIGLU, OG.EPI_GELU_F16])
-def test_gemm_s8_transcendental_epilogues(dev, rng, epi):
-    M, N, K = 513, 5632, 1024
+def test_gemm_s8_gelu_epilogue(dev, rng):
+    M, N, K = 513, 4736, 1024
     a, w, rs, cs, bias = gemm_inputs(rng, M, N, K)
-    got = run_gemm(dev, a, w, rs, cs, bias, epi, 0).astype(np.float32)
-    want = OG.gemm_s8(a, w, rs, cs, bias, epi).astype(np.float32)
+    got = run_gemm(dev, a, w, rs, cs, bias, OG.EPI_GELU_F16, 0).astype(np.float32)
+    want = OG.gemm_s8(a, w, rs, cs, bias, OG.EPI_GELU_F16).astype(np.float32)
     np.testing.assert_allclose(got, want, rtol=1e-3, atol=1e-4)
 
 
