@@ -1,0 +1,47 @@
+"""ROCm backend: the gfx950 int8 engine behind the reference's Backend protocol.
+
+Mirrors CUDABackend (foidfinder/backends/cuda/__init__.py:15-43): constructor (model_dir) raising RuntimeError with
+a readable message when unsupported, `name`, `device`, and `predict(image) -> float32 probabilities [num_tags]`
+(sigmoid applied), called from one thread. Adds `predict_batch(images) -> [B, num_tags]` for batched serving.
+"""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from .preprocess import preprocess
+
+
+class ROCmBackend:
+    name = "rocm"
+
+    def __init__(self, model_dir: Path):
+        if not torch.cuda.is_available() or not torch.version.hip:
+            raise RuntimeError("ROCm backend: no AMD GPU visible (needs a ROCm build of PyTorch)")
+        arch = torch.cuda.get_device_properties(0).gcnArchName.split(":")[0]
+        if arch != "gfx950":
+            raise RuntimeError(f"ROCm backend: kernels are built for gfx950 (MI355X), found {arch}")
+        config = json.loads((Path(model_dir) / "config.json").read_text())
+        arch_name = config.get("model", {}).get("architecture")
+        if arch_name != "eva02-int8":
+            raise RuntimeError(
+                f"ROCm backend runs int8 EVA02 taggers (config architecture 'eva02-int8'), not {arch_name!r}"
+            )
+        from ...engine import load_model_dir
+
+        self.engine, self.config = load_model_dir(model_dir)
+        self.size = self.engine.cfg.img_size
+        self.device = torch.cuda.get_device_name()
+
+    @torch.no_grad()
+    def predict(self, image) -> np.ndarray:
+        return self.predict_batch([image])[0]
+
+    @torch.no_grad()
+    def predict_batch(self, images: list) -> np.ndarray:
+        logits = self.engine(preprocess(images, self.size))
+        return torch.sigmoid(logits).cpu().numpy()

@@ -288,8 +288,8 @@ extern "C" int ff_gemm_s8(const int8_t* A, const int8_t* W, int64_t M, int64_t N
   a.q_scale = q_scale;
   hipStream_t st = as_stream(stream);
   switch (variant) {
-    case 0:
     case 1: return launch_epi<256, 128>(a, epi, st);
+    case 0:
     case 2: return launch_epi<128, 128>(a, epi, st);
   }
   return fail(FF_EINVAL, "gemm_s8: bad variant");
