@@ -19,7 +19,9 @@ constexpr int BQ = 128;         // queries per workgroup
 constexpr int BKV = 64;         // keys per tile
 constexpr int VT_STRIDE = 68;   // halves per transposed-V row: 64 keys + 4 pad (136 B rows spread the banks)
 
-__device__ __forceinline__ int k_swz(int row, int chunk) { return row * HD + ((chunk ^ (row & 7)) << 3); }
+// K tile rows of 128 B (8 chunks of 16 B), chunk XOR bits 1-3 of the row: the 16 lanes of one 16-byte LDS read pass
+// (64 banks, 256 B) read 16 rows -> 2 rows per 256-byte window, spread over 16 distinct slots.
+__device__ __forceinline__ int k_swz(int row, int chunk) { return row * HD + ((chunk ^ ((row >> 1) & 7)) << 3); }
 
 __global__ __launch_bounds__(256) void attention_kernel(const half_t* __restrict__ qkv, half_t* __restrict__ out,
                                                         int L, int H) {
@@ -27,7 +29,11 @@ __global__ __launch_bounds__(256) void attention_kernel(const half_t* __restrict
   __shared__ __attribute__((aligned(16))) half_t sV[2][HD * VT_STRIDE];
 
   const int C = H * HD, ROW = 3 * C;
-  const int qb = blockIdx.x, h = blockIdx.y, seq = blockIdx.z;
+  // 1-D grid over (sequence, head, query block), query block fastest, remapped so that all query blocks of one
+  // (sequence, head) run on one XCD and read its K and V through one L2.
+  const int nq = (L + BQ - 1) / BQ;
+  const int t = xcd_remap(blockIdx.x, gridDim.x);
+  const int qb = t % nq, h = (t / nq) % H, seq = t / (nq * H);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 31, fh = lane >> 5;
   const int64_t tok0 = static_cast<int64_t>(seq) * L;
@@ -170,13 +176,13 @@ extern "C" int ff_attention(const void* qkv, void* out, int64_t T, int64_t heads
   if (T < 0 || T % seq_len != 0) return fail(FF_EINVAL, "attention: T must be a multiple of seq_len");
   if (heads * 3 * HD * seq_len > (int64_t(1) << 40)) return fail(FF_EINVAL, "attention: too large");
   const int64_t seqs = T / seq_len;
-  if (seqs > 65535) return fail(FF_EINVAL, "attention: more than 65535 sequences");
   if (T == 0) return FF_OK;
   if (!qkv || !out) return fail(FF_EINVAL, "attention: null pointer");
   if ((reinterpret_cast<uintptr_t>(qkv) & 15) || (reinterpret_cast<uintptr_t>(out) & 7))
     return fail(FF_EINVAL, "attention: misaligned pointer");
-  const dim3 grid(static_cast<unsigned>((seq_len + BQ - 1) / BQ), static_cast<unsigned>(heads),
-                  static_cast<unsigned>(seqs));
+  const int64_t blocks = (seq_len + BQ - 1) / BQ * heads * seqs;
+  if (blocks > 0x7fffffff) return fail(FF_EINVAL, "attention: too many blocks");
+  const dim3 grid(static_cast<unsigned>(blocks));
   attention_kernel<<<grid, 256, 0, as_stream(stream)>>>(static_cast<const half_t*>(qkv), static_cast<half_t*>(out),
                                                         static_cast<int>(seq_len), static_cast<int>(heads));
   return check_launch("attention");

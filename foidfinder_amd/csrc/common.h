@@ -30,16 +30,13 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 // ---- device helpers ----
 
-// Round to nearest even, clamp to [-127, 127], and keep the low byte (two's complement).
-__device__ __forceinline__ uint32_t q8(float v) {
-  int q = static_cast<int>(__builtin_rintf(v));
-  q = q < -127 ? -127 : (q > 127 ? 127 : q);
-  return static_cast<uint32_t>(q) & 0xffu;
-}
-
-// Four codes packed little-endian into one dword.
-__device__ __forceinline__ uint32_t q8x4(float a, float b, float c, float d) {
-  return q8(a) | (q8(b) << 8) | (q8(c) << 16) | (q8(d) << 24);
+// Workgroups are dispatched round-robin over the 8 XCDs (block b runs on XCD b % 8), each with its own L2. This
+// bijection gives XCD x the contiguous run of logical work items [x*q + min(x, r), ...), so work items that share
+// operands (GEMM tiles of one panel, query blocks of one attention head) share one L2.
+__device__ __forceinline__ int xcd_remap(int b, int nblocks) {
+  const int q = nblocks >> 3, r = nblocks & 7;
+  const int x = b & 7, k = b >> 3;
+  return x * q + (x < r ? x : r) + k;
 }
 
 // Value of lane (lane ^ mask) within the wave (ds_bpermute).

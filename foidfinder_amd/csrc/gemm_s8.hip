@@ -5,13 +5,21 @@
 // -ffp-contract=off), then the epilogue. The integer part is exact, so the order of the k-sum is free: each lane
 // feeds the MFMA 16 contiguous bytes of K and the A- and W-fragments use the same k slots.
 //
-// Tiling: a 256-thread workgroup (4 waves as 2 x 2) computes a BM x BN tile of C from BK = 64 byte K-slices,
-// double-buffered in LDS (global -> registers -> LDS, so the next slice's loads are in flight during the MFMAs).
-// Each wave owns a (BM/2) x (BN/2) sub-tile made of 32 x 32 blocks of v_mfma_i32_32x32x32_i8. The MFMA computes the
-// transposed product D[n][m] (W fragment as the row operand), so each lane ends with one row m and runs of 4
-// consecutive columns n: pair epilogues (RoPE, SwiGLU) stay inside a lane and stores are 8 bytes wide.
+// Both kernels use 256-thread workgroups (4 waves as 2 x 2), 64-byte K slices in LDS with the 16-byte chunks of
+// each 64-byte row XOR-swizzled by bits 2-3 of the row (conflict-free 16-byte fragment reads), and
+// v_mfma_i32_32x32x32_i8 computing the transposed product D[n][m] (the W fragment is the row operand), so each lane
+// ends with one output row m and runs of 4 consecutive columns n: the pair epilogues (RoPE, SwiGLU) stay inside a
+// lane and stores are 8 bytes wide.
+//
+//  * gemm_s8_pipe_kernel (variant 1, large M): 256 x 256 tiles, each wave a 128 x 128 sub-tile (16 accumulator
+//    blocks in AGPRs), a 4-stage LDS ring filled by direct global->LDS loads (global_load_lds_dwordx4: no VGPR
+//    staging, 3 slices in flight). Tiles are ordered per XCD in groups of 4 m-tiles x 8 n-tiles so the 32 tiles an
+//    XCD runs at once share their A and W panels in its L2.
+//  * gemm_s8_kernel (variants 2, 3, small M): 128 x 128 or 256 x 128 tiles, register-staged double buffering.
 //
 // Reference: foidfinder/backends/cuda/csrc/gemm.cuh:14-171 and kernels.cu:167-217.
+#include <type_traits>
+
 #include "common.h"
 
 namespace ff {
@@ -32,17 +40,12 @@ struct GemmArgs {
 
 constexpr int BK = 64;
 
-// LDS rows of 64 bytes (4 chunks of 16 B); chunk index XOR-swizzled with bits 1-2 of the row so the 16-byte
-// fragment reads of 8 consecutive rows hit distinct banks.
-__device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ ((row >> 1) & 3)) << 4); }
-
-// Workgroups are dispatched round-robin over the 8 XCDs; give each XCD a contiguous run of tiles (n fastest) so
-// the tiles sharing an A row-panel share one L2.
-__device__ __forceinline__ int xcd_remap(int b, int nblocks) {
-  const int q = nblocks >> 3, r = nblocks & 7;
-  const int x = b & 7, k = b >> 3;
-  return x * q + (x < r ? x : r) + k;
-}
+// LDS rows of 64 bytes (4 chunks of 16 B); chunk index XOR-swizzled with bits 2-3 of the row. gfx950 serves a
+// 16-byte-per-lane LDS read 16 lanes at a time from 64 four-byte banks (256 B), so the 16 rows read by 16 consecutive
+// lanes must land in 16 distinct 16-byte slots of a 256-byte window: rows r..r+3 fill one window's 4 slots each, and
+// the XOR with (r >> 2) & 3 spreads r, r+4, r+8, r+12 over the 4 chunk positions (measured: zero bank conflicts,
+// where XOR with bits 1-2 doubles every read).
+__device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ ((row >> 2) & 3)) << 4); }
 
 // exp(x) from plain fp32 operations in a fixed order (no fused multiply-add: this file is built with
 // -ffp-contract=off), so the CPU oracle reproduces it bit for bit: Cody-Waite range reduction x = n ln2 + r with ln2
@@ -67,6 +70,258 @@ __device__ __forceinline__ float silu(float g) { return g / (1.f + exp_cw(-g)); 
 __device__ __forceinline__ float gelu_tanh(float y) {
   return 0.5f * y * (1.f + tanhf(0.7978845608f * (y + 0.044715f * y * y * y)));
 }
+
+// Per-wave LDS staging area of store_epilogue: 32 rows of the wave's output columns, each row padded by 8 bytes so
+// the 8-byte writes of 32 lanes (32 rows, one column group) and the 16-byte row reads both hit 64 distinct banks.
+template <int EPI, int NI>
+constexpr int stage_row_bytes() {
+  return (EPI == FF_EPI_SWIGLU ? NI * 16 : NI * 32) * 2 + 8;
+}
+template <int EPI, int NI>
+constexpr int stage_bytes() {
+  return 32 * stage_row_bytes<EPI, NI>();
+}
+
+// The epilogue of one wave: acc[i][j][4q + t] is D[n][m] with m = m_base + 32j + (lane & 31) and
+// n = n_base + 32i + 8q + 4*(lane >> 5) + t. For each 32-row block j the wave computes y and the fp16 results in
+// registers (pairs of columns are in-lane for RoPE and SwiGLU), writes them to its LDS staging area, and then stores
+// whole 16-byte row segments (for RESIDUAL: loads the matching residual segment and adds in fp16), so global stores
+// are row-contiguous instead of 16 bytes per row. `stage` is this wave's private area of stage_bytes<EPI, NI>().
+template <int EPI, int NI, int MI>
+__device__ __forceinline__ void store_epilogue(const int16_t_v (&acc)[NI][MI], int m_base, int n_base, int lane,
+                                               const GemmArgs& args, uint8_t* stage) {
+  const int M = args.M, N = args.N;
+  const int fr = lane & 31, fk = lane >> 5;
+  if constexpr (EPI == FF_EPI_I32) {  // debug output: raw accumulators, stored from registers
+#pragma unroll
+    for (int j = 0; j < MI; ++j) {
+      const int m = m_base + 32 * j + fr;
+      if (m >= M) continue;
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n = n_base + 32 * i + 8 * q + 4 * fk;
+          if (n >= N) continue;
+          int4_t v;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) v[t] = acc[i][j][4 * q + t];
+          *reinterpret_cast<int4_t*>(static_cast<int*>(args.out) + static_cast<int64_t>(m) * N + n) = v;
+        }
+    }
+    return;
+  } else {
+    constexpr bool SWI = EPI == FF_EPI_SWIGLU;
+    constexpr int RB = stage_row_bytes<EPI, NI>();
+    constexpr int OUT_COLS = SWI ? NI * 16 : NI * 32;  // fp16 output columns of the wave
+    constexpr int LANES_PER_ROW = OUT_COLS / 8;        // 16-byte segments per row
+    constexpr int ROWS_PER_PASS = 64 / LANES_PER_ROW;
+    const int out_ld = SWI ? N / 2 : N;
+    const int out_n0 = SWI ? n_base / 2 : n_base;
+    const int C3 = N / 3;  // QKV: section width
+    half_t* o16 = static_cast<half_t*>(args.out);
+#pragma unroll
+    for (int j = 0; j < MI; ++j) {
+      const int mrow = m_base + 32 * j + fr;
+      const int m = min(mrow, M - 1);  // rows past M are computed on clamped inputs and never stored
+      const float rs = args.row_scale[m];
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int c = 32 * i + 8 * q + 4 * fk;  // column within the wave's tile
+          const int n = min(n_base + c, N - 4);   // past-N columns: clamped reads, never stored
+          const float4_t cs = *reinterpret_cast<const float4_t*>(args.col_scale + n);
+          const float4_t bi = *reinterpret_cast<const float4_t*>(args.bias + n);
+          float y[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) y[t] = static_cast<float>(acc[i][j][4 * q + t]) * rs * cs[t] + bi[t];
+          if constexpr (SWI) {
+            half2_t h;
+            h[0] = static_cast<half_t>(silu(y[0]) * y[1]);
+            h[1] = static_cast<half_t>(silu(y[2]) * y[3]);
+            *reinterpret_cast<half2_t*>(stage + fr * RB + c) = h;  // output column c/2, 2 bytes each
+          } else {
+            if constexpr (EPI == FF_EPI_QKV_ROPE) {
+              const int section = n / C3;
+              if (section < 2) {
+                const int trow = (m % args.rope_len) * 32 + ((n & 63) >> 1);
+#pragma unroll
+                for (int pr = 0; pr < 2; ++pr) {
+                  const float co = args.rope_cos[trow + pr], si = args.rope_sin[trow + pr];
+                  const float y0 = y[2 * pr], y1 = y[2 * pr + 1];
+                  const float r0 = y0 * co - y1 * si, r1 = y0 * si + y1 * co;
+                  const float qs = section == 0 ? args.q_scale : 1.f;
+                  y[2 * pr] = section == 0 ? r0 * qs : r0;
+                  y[2 * pr + 1] = section == 0 ? r1 * qs : r1;
+                }
+              }
+            }
+            if constexpr (EPI == FF_EPI_GELU_F16) {
+#pragma unroll
+              for (int t = 0; t < 4; ++t) y[t] = gelu_tanh(y[t]);
+            }
+            half4_t h;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) h[t] = static_cast<half_t>(y[t]);
+            *reinterpret_cast<half4_t*>(stage + fr * RB + 2 * c) = h;
+          }
+        }
+      __builtin_amdgcn_wave_barrier();
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int p = 0; p < 32 / ROWS_PER_PASS; ++p) {
+        const int r = p * ROWS_PER_PASS + lane / LANES_PER_ROW;
+        const int seg = lane % LANES_PER_ROW;
+        half8_t h = *reinterpret_cast<const half8_t*>(stage + r * RB + seg * 16);
+        const int gm = m_base + 32 * j + r, gn = out_n0 + seg * 8;
+        if (gm < M && gn < out_ld) {
+          half8_t* dst = reinterpret_cast<half8_t*>(o16 + static_cast<int64_t>(gm) * out_ld + gn);
+          if constexpr (EPI == FF_EPI_RESIDUAL) {
+            const half8_t x = *dst;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) h[t] = h[t] + x[t];
+          }
+          *dst = h;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+  }
+}
+
+// ---------------- variant 1: 256 x 256 tiles, 4-stage direct-to-LDS pipeline ----------------
+
+constexpr int P_BM = 256, P_BN = 256, P_STAGES = 4;
+constexpr int P_STAGE = (P_BM + P_BN) * BK;    // 32 KB per stage
+constexpr int P_LOADS = P_STAGE / (256 * 16);  // 16-byte loads per thread per stage (8)
+constexpr int P_GROUP_M = 4;                   // m-tiles per tile group (an XCD runs ~32 tiles at once)
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Issues this thread's share of one K slice: rows of A (m0..m0+255) then W (n0..n0+255), 64 bytes each. A wave's
+// global_load_lds_dwordx4 writes 1 KB of LDS contiguously (lane l at +16 l), i.e. 16 rows; the lane reads the
+// global chunk that the swizzle places at its LDS position.
+__device__ __forceinline__ void pipe_issue(uint8_t* stage_base, const GemmArgs& a, int m0, int n0, int kt, int wave,
+                                           int lane) {
+  const int r16 = lane >> 2, pc = lane & 3;
+#pragma unroll
+  for (int p = 0; p < P_LOADS; ++p) {
+    const int blk = wave * P_LOADS + p;  // 1 KB block of the stage: 0..15 A rows, 16..31 W rows
+    const int row = (blk & 15) * 16 + r16;
+    const int lc = pc ^ ((row >> 2) & 3);  // the chunk swz() places at this lane's LDS position
+    const int8_t* src;
+    if (blk < 16) {
+      const int m = min(m0 + row, a.M - 1);
+      src = a.A + static_cast<int64_t>(m) * a.K + kt * BK + lc * 16;
+    } else {
+      const int n = min(n0 + row, a.N - 1);
+      src = a.W + static_cast<int64_t>(n) * a.K + kt * BK + lc * 16;
+    }
+    __builtin_amdgcn_global_load_lds(src, (lds_void*)(stage_base + blk * 1024), 16, 0, 0);
+  }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256, 1) void gemm_s8_pipe_kernel(const GemmArgs args) {
+  constexpr int WM = P_BM / 2, WN = P_BN / 2, MI = WM / 32, NI = WN / 32;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[P_STAGES * P_STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tiles_m = (args.M + P_BM - 1) / P_BM, tiles_n = (args.N + P_BN - 1) / P_BN;
+  // logical tile -> (tm, tn): groups of P_GROUP_M m-tiles, m fastest within a group
+  const int t = xcd_remap(blockIdx.x, gridDim.x);
+  const int per_group = P_GROUP_M * tiles_n;
+  const int g = t / per_group, in_g = t % per_group;
+  const int gm = min(P_GROUP_M, tiles_m - g * P_GROUP_M);
+  const int tm = g * P_GROUP_M + in_g % gm, tn = in_g / gm;
+  const int m0 = tm * P_BM, n0 = tn * P_BN;
+  const int KT = args.K / BK;
+
+  int16_t_v acc[NI][MI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+#pragma unroll
+    for (int j = 0; j < MI; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+#pragma unroll
+  for (int s = 0; s < P_STAGES - 1; ++s)
+    if (s < KT) pipe_issue(smem + s * P_STAGE, args, m0, n0, s, wave, lane);
+
+  // Fragment reads are software-pipelined against the MFMAs: the second K half of slice kt is read while the first
+  // half's 16 MFMAs run, and the first half of slice kt+1 while the second half's run (2 MFMAs : 1 ds_read).
+  const int fr = lane & 31, fk = lane >> 5;
+  int4_t xw0[NI], ya0[MI], xw1[NI], ya1[MI];
+  auto read_half = [&](int slot, int kk, int4_t (&xw)[NI], int4_t (&ya)[MI]) {
+    const uint8_t* sa = smem + slot * P_STAGE;
+    const uint8_t* sw = sa + P_BM * BK;
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      xw[i] = *reinterpret_cast<const int4_t*>(sw + swz(wn * WN + i * 32 + fr, 2 * kk + fk));
+#pragma unroll
+    for (int j = 0; j < MI; ++j)
+      ya[j] = *reinterpret_cast<const int4_t*>(sa + swz(wm * WM + j * 32 + fr, 2 * kk + fk));
+  };
+  auto mfma_half = [&](const int4_t (&xw)[NI], const int4_t (&ya)[MI]) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int j = 0; j < MI; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xw[i], ya[j], acc[i][j], 0, 0, 0);
+  };
+  auto interleave = [] {
+#pragma unroll
+    for (int x = 0; x < NI + MI; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // 2 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
+    }
+  };
+  auto barrier = [] {
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  // Slice 0 is in LDS once this thread's loads of it are done and every thread has passed the barrier.
+  if (KT >= P_STAGES - 1)
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((P_STAGES - 2) * P_LOADS) : "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  barrier();
+  read_half(0, 0, xw0, ya0);
+
+  // One K slice. STEADY: slices kt+1..kt+P_STAGES-1 exist, so the refill of slot (kt-1) % P_STAGES (last read before
+  // the previous barrier) is issued and the wait for slice kt+1 may leave the newer (P_STAGES - 2) slices in flight;
+  // otherwise (the last P_STAGES - 1 slices) nothing is issued and the wait drains. Branch-free inside, so each half
+  // is one scheduling region. On the last slice the reads of "slice kt+1" hit a stale slot and are never used.
+  auto step = [&](int kt, auto steady) {
+    if constexpr (decltype(steady)::value)
+      pipe_issue(smem + ((kt + P_STAGES - 1) % P_STAGES) * P_STAGE, args, m0, n0, kt + P_STAGES - 1, wave, lane);
+    read_half(kt % P_STAGES, 1, xw1, ya1);
+    mfma_half(xw0, ya0);
+    interleave();
+    // This thread's reads of slot kt are complete before the barrier, so no thread refills it while it is read.
+    if constexpr (decltype(steady)::value)
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((P_STAGES - 2) * P_LOADS) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    barrier();
+    read_half((kt + 1) % P_STAGES, 0, xw0, ya0);
+    mfma_half(xw1, ya1);
+    interleave();
+  };
+  int kt = 0;
+  for (; kt + P_STAGES - 1 < KT; ++kt) step(kt, std::true_type{});
+  for (; kt < KT; ++kt) step(kt, std::false_type{});
+  __syncthreads();  // every wave is done with the ring; reuse it as the epilogue staging area
+  store_epilogue<EPI, NI, MI>(acc, m0 + wm * WM, n0 + wn * WN, lane, args,
+                              smem + wave * stage_bytes<EPI, NI>());
+}
+
+// ---------------- variants 2, 3: register-staged double buffering ----------------
 
 template <int BM, int BN, int EPI>
 __global__ __launch_bounds__(256) void gemm_s8_kernel(const GemmArgs args) {
@@ -155,76 +410,13 @@ __global__ __launch_bounds__(256) void gemm_s8_kernel(const GemmArgs args) {
     if (kt + 1 < KT) swrite(cur ^ 1);
     __syncthreads();
   }
-
-  // Epilogue from registers. acc[i][j][4q + t] is D[n][m] with m = m0 + wm*WM + 32j + (lane & 31) and
-  // n = n0 + wn*WN + 32i + 8q + 4*(lane >> 5) + t.
-  const int C3 = N / 3;  // QKV: section width
-#pragma unroll
-  for (int j = 0; j < MI; ++j) {
-    const int m = m0 + wm * WM + 32 * j + fr;
-    if (m >= M) continue;
-    const float rs = args.row_scale[m];
-#pragma unroll
-    for (int i = 0; i < NI; ++i)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * WN + 32 * i + 8 * q + 4 * fk;
-        if (n >= N) continue;
-        if constexpr (EPI == FF_EPI_I32) {
-          int4_t v;
-#pragma unroll
-          for (int t = 0; t < 4; ++t) v[t] = acc[i][j][4 * q + t];
-          *reinterpret_cast<int4_t*>(static_cast<int*>(args.out) + static_cast<int64_t>(m) * N + n) = v;
-        } else {
-          const float4_t cs = *reinterpret_cast<const float4_t*>(args.col_scale + n);
-          const float4_t bi = *reinterpret_cast<const float4_t*>(args.bias + n);
-          float y[4];
-#pragma unroll
-          for (int t = 0; t < 4; ++t) y[t] = static_cast<float>(acc[i][j][4 * q + t]) * rs * cs[t] + bi[t];
-          half_t* o16 = static_cast<half_t*>(args.out);
-          if constexpr (EPI == FF_EPI_SWIGLU) {
-            half2_t h;
-            h[0] = static_cast<half_t>(silu(y[0]) * y[1]);
-            h[1] = static_cast<half_t>(silu(y[2]) * y[3]);
-            *reinterpret_cast<half2_t*>(o16 + static_cast<int64_t>(m) * (N / 2) + n / 2) = h;
-          } else {
-            if constexpr (EPI == FF_EPI_QKV_ROPE) {
-              const int section = n / C3;
-              if (section < 2) {
-                const int trow = (m % args.rope_len) * 32 + ((n & 63) >> 1);
-#pragma unroll
-                for (int pr = 0; pr < 2; ++pr) {
-                  const float co = args.rope_cos[trow + pr], si = args.rope_sin[trow + pr];
-                  const float y0 = y[2 * pr], y1 = y[2 * pr + 1];
-                  const float r0 = y0 * co - y1 * si, r1 = y0 * si + y1 * co;
-                  const float qs = section == 0 ? args.q_scale : 1.f;
-                  y[2 * pr] = section == 0 ? r0 * qs : r0;
-                  y[2 * pr + 1] = section == 0 ? r1 * qs : r1;
-                }
-              }
-            }
-            if constexpr (EPI == FF_EPI_GELU_F16) {
-#pragma unroll
-              for (int t = 0; t < 4; ++t) y[t] = gelu_tanh(y[t]);
-            }
-            half4_t h;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) h[t] = static_cast<half_t>(y[t]);
-            half4_t* dst = reinterpret_cast<half4_t*>(o16 + static_cast<int64_t>(m) * N + n);
-            if constexpr (EPI == FF_EPI_RESIDUAL) {
-              const half4_t x = *dst;
-#pragma unroll
-              for (int t = 0; t < 4; ++t) h[t] = h[t] + x[t];
-            }
-            *dst = h;
-          }
-        }
-      }
-  }
+  static_assert(4 * stage_bytes<FF_EPI_QKV_ROPE, NI>() <= 2 * STAGE, "staging must fit in the tile buffers");
+  store_epilogue<EPI, NI, MI>(acc, m0 + wm * WM, n0 + wn * WN, lane, args,
+                              reinterpret_cast<uint8_t*>(smem) + wave * stage_bytes<EPI, NI>());
 }
 
 template <int BM, int BN>
-static int launch_epi(const GemmArgs& a, int epi, hipStream_t st) {
+static int launch_staged(const GemmArgs& a, int epi, hipStream_t st) {
   const int64_t tiles = static_cast<int64_t>((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   if (tiles > 0x7fffffff) return fail(FF_EINVAL, "gemm_s8: too many tiles");
   const dim3 grid(static_cast<unsigned>(tiles));
@@ -240,7 +432,24 @@ static int launch_epi(const GemmArgs& a, int epi, hipStream_t st) {
   return check_launch("gemm_s8");
 }
 
-constexpr int kVariants = 2;  // 1: 256 x 128 tiles, 2: 128 x 128 tiles
+static int launch_pipe(const GemmArgs& a, int epi, hipStream_t st) {
+  const int64_t tiles = static_cast<int64_t>((a.M + P_BM - 1) / P_BM) * ((a.N + P_BN - 1) / P_BN);
+  if (tiles > 0x7fffffff) return fail(FF_EINVAL, "gemm_s8: too many tiles");
+  const dim3 grid(static_cast<unsigned>(tiles));
+  switch (epi) {
+    case FF_EPI_QKV_ROPE: gemm_s8_pipe_kernel<FF_EPI_QKV_ROPE><<<grid, 256, 0, st>>>(a); break;
+    case FF_EPI_RESIDUAL: gemm_s8_pipe_kernel<FF_EPI_RESIDUAL><<<grid, 256, 0, st>>>(a); break;
+    case FF_EPI_GELU_F16: gemm_s8_pipe_kernel<FF_EPI_GELU_F16><<<grid, 256, 0, st>>>(a); break;
+    case FF_EPI_SWIGLU: gemm_s8_pipe_kernel<FF_EPI_SWIGLU><<<grid, 256, 0, st>>>(a); break;
+    case FF_EPI_BIAS_F16: gemm_s8_pipe_kernel<FF_EPI_BIAS_F16><<<grid, 256, 0, st>>>(a); break;
+    case FF_EPI_I32: gemm_s8_pipe_kernel<FF_EPI_I32><<<grid, 256, 0, st>>>(a); break;
+    default: return fail(FF_EINVAL, "gemm_s8: bad epilogue");
+  }
+  return check_launch("gemm_s8");
+}
+
+// 1: 256 x 256 pipelined (direct-to-LDS, 4 stages); 2: 128 x 128 staged; 3: 256 x 128 staged.
+constexpr int kVariants = 3;
 
 }  // namespace ff
 
@@ -287,10 +496,11 @@ extern "C" int ff_gemm_s8(const int8_t* A, const int8_t* W, int64_t M, int64_t N
   a.rope_len = static_cast<int>(rope_len);
   a.q_scale = q_scale;
   hipStream_t st = as_stream(stream);
+  if (variant == 0) variant = M >= 4096 ? 1 : 2;
   switch (variant) {
-    case 1: return launch_epi<256, 128>(a, epi, st);
-    case 0:
-    case 2: return launch_epi<128, 128>(a, epi, st);
+    case 1: return launch_pipe(a, epi, st);
+    case 2: return launch_staged<128, 128>(a, epi, st);
+    case 3: return launch_staged<256, 128>(a, epi, st);
   }
   return fail(FF_EINVAL, "gemm_s8: bad variant");
 }

@@ -1,26 +1,57 @@
 // Walsh-Hadamard rotation fused with per-token symmetric int8 quantization (gfx950, wave64).
 //
 // The rotation spreads activation outliers over all channels so one scale per token suffices; the weights carry the
-// same rotation. Both kernels are HBM-bound (2 B read + 1 B written per element). The butterfly stage order, the
-// LayerNorm reduction order and every rounding match oracle/rotq8.py bit for bit (this file is compiled with
-// -ffp-contract=off and correctly rounded fp32 division and sqrt).
+// same rotation. Both kernels are HBM-bound in bytes (2 B read + 1 B written per element) and close to VALU-bound
+// in instructions, so the cross-lane butterflies are single DPP operations:
+//
+//  * Gray-code lane order: lane l of a 16-lane DPP row owns the 16-byte column chunk gray(l) = l ^ (l >> 1) of its
+//    128-column group. The butterfly partner for column bit 3, 4, 5, 6 is then lane l ^ 1, ^ 3, ^ 7, ^ 15: quad_perm,
+//    quad_perm, row_half_mirror and row_mirror, each a DPP source modifier (no LDS traffic, no extra instruction).
+//  * Sign tracking: with partner value p and own value u, every lane computes fma(p, s, u) with s = +1 if its column
+//    bit is 0 and -1 if 1. The lower lane gets a + b; the upper gets b - a = -(a - b), i.e. the reference's a - b
+//    negated. One instruction per value and stage; the accumulated sign (-1)^(number of set column bits) is folded
+//    into the quantization multiplier and the absmax is sign-free, so codes and scales are unchanged bit for bit
+//    (IEEE rounding is sign-symmetric and fma(p, +-1, u) rounds once, like the reference's add and subtract).
+//
+// The butterfly stage order, the LayerNorm reduction order and every rounding match oracle/rotq8.py bit for bit (this
+// file is compiled with -ffp-contract=off and correctly rounded fp32 division and sqrt).
 //
 // Reference: foidfinder/backends/cuda/csrc/kernels.cu:13-160 (rot_q8_1024_kernel, rot_q8_h128_kernel).
 #include "common.h"
 
 namespace ff {
 
-// Sum over the 32 lanes of a half-wave, xor tree 16, 8, 4, 2, 1 (the order fixes the rounding).
-__device__ __forceinline__ float half_wave_sum(float v) {
-#pragma unroll
-  for (int m = 16; m; m >>= 1) v = v + xor_shuffle(v, m);
-  return v;
+// DPP controls: partner lane l ^ 1, l ^ 3 (quad_perm), l ^ 7 (row_half_mirror), l ^ 15 (row_mirror).
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR3 = 0x1B, DPP_XOR7 = 0x141, DPP_XOR15 = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
-__device__ __forceinline__ float half_wave_max(float v) {
-#pragma unroll
-  for (int m = 16; m; m >>= 1) v = fmaxf(v, xor_shuffle(v, m));
-  return v;
+// Value of lane l ^ 16 within a 32-lane group (ds_swizzle bitmask mode: and 0x1F, or 0, xor 0x10).
+__device__ __forceinline__ float swz_xor16(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+
+// Sign-tracked butterfly across lanes: partner p, own u, s = +1 (column bit 0) or -1 (column bit 1).
+template <int CTRL>
+__device__ __forceinline__ float bfly(float u, float s) {
+  return __builtin_fmaf(dpp<CTRL>(u), s, u);
+}
+
+__device__ __forceinline__ float gray_sign(int bit) { return bit ? -1.f : 1.f; }
+
+// Code of t in [-inf, inf]: clamp to [-127, 127], round half to even, low byte. Adding 1.5 * 2^23 rounds to an
+// integer with ties to even (the ulp there is 1 and 1.5 * 2^23 is even), and the low byte of the sum's bit pattern is
+// the code in two's complement.
+__device__ __forceinline__ uint32_t q8_fast(float t) {
+  const float c = __builtin_amdgcn_fmed3f(t, -127.f, 127.f) + 12582912.f;
+  return __builtin_bit_cast(uint32_t, c) & 0xffu;
+}
+
+__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d) {
+  return q8_fast(a) | (q8_fast(b) << 8) | (q8_fast(c) << 16) | (q8_fast(d) << 24);
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -35,27 +66,44 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// Butterfly across lanes: the lane with bit `m` clear holds a, its partner b; results a + b (lower), a - b (upper).
-__device__ __forceinline__ float lane_butterfly(float v, int m, bool upper) {
-  const float o = xor_shuffle(v, m);
-  return upper ? o - v : v + o;
+// The LayerNorm reduction of the reference (kernels.cu:73, common.cuh:58-62) pairs reference lanes L ^ 16, ^ 8, ^ 4,
+// ^ 2, ^ 1. With the Gray lane order those partners are physical lanes l ^ 16, ^ 15, ^ 7, ^ 3, ^ 1.
+__device__ __forceinline__ float ref_tree_sum(float v) {
+  v = v + swz_xor16(v);
+  v = v + dpp<DPP_XOR15>(v);
+  v = v + dpp<DPP_XOR7>(v);
+  v = v + dpp<DPP_XOR3>(v);
+  v = v + dpp<DPP_XOR1>(v);
+  return v;
 }
 
-// One row of 1024 per 32-lane half-wave; lane L of the half owns columns j*256 + L*8 + e (j 0..3, e 0..7), the
-// reference's column layout (kernels.cu:11-12), which makes its stage order (column bits 0,1,2 | 8,9 | 3..7) and its
-// LayerNorm reduction order natural here. 8 rows per 256-thread workgroup.
+__device__ __forceinline__ float half_wave_max(float v) {
+  v = fmaxf(v, swz_xor16(v));
+  v = fmaxf(v, dpp<DPP_XOR15>(v));
+  v = fmaxf(v, dpp<DPP_XOR7>(v));
+  v = fmaxf(v, dpp<DPP_XOR3>(v));
+  v = fmaxf(v, dpp<DPP_XOR1>(v));
+  return v;
+}
+
+// One row of 1024 per 32-lane half-wave. Reference lane L = 16 c7 + gray(l & 15) of the half owns columns
+// j*256 + L*8 + e (j 0..3, e 0..7), the reference's column layout (kernels.cu:11-12), held by physical lane
+// l = 16 c7 + gray^-1(L & 15). Stage order: column bits 0, 1, 2 (registers e), 8, 9 (registers j), 3..7 (lanes; the
+// last one, bit 7 = lane bit 4, through ds_swizzle). 8 rows per 256-thread workgroup.
 template <bool NORM>
 __global__ __launch_bounds__(256) void rot_q8_1024_kernel(const half_t* __restrict__ x, const float* __restrict__ gamma,
                                                           const float* __restrict__ beta, float eps, int64_t T,
                                                           int8_t* __restrict__ out, float* __restrict__ row_scale) {
   const int lane = threadIdx.x & 31;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 5);
-  if (row >= T) return;  // whole half-waves exit together; shuffles below stay inside the half
+  if (row >= T) return;  // whole half-waves exit together; cross-lane operations below stay inside the half
+  const int l16 = lane & 15, gl = l16 ^ (l16 >> 1);
+  const int L = (lane & 16) | gl;  // reference lane = column bits 3..7
   const half_t* xr = x + row * 1024;
   float v[32];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const half8_t h = *reinterpret_cast<const half8_t*>(xr + j * 256 + lane * 8);
+    const half8_t h = *reinterpret_cast<const half8_t*>(xr + j * 256 + L * 8);
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[j * 8 + e] = static_cast<float>(h[e]);
   }
@@ -63,18 +111,18 @@ __global__ __launch_bounds__(256) void rot_q8_1024_kernel(const half_t* __restri
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < 32; ++i) s = s + v[i];
-    const float mean = half_wave_sum(s) * (1.f / 1024.f);
+    const float mean = ref_tree_sum(s) * (1.f / 1024.f);
     float sq = 0.f;
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
       v[i] = v[i] - mean;
       sq = sq + v[i] * v[i];
     }
-    const float var = half_wave_sum(sq) * (1.f / 1024.f);
+    const float var = ref_tree_sum(sq) * (1.f / 1024.f);
     const float rstd = 1.f / sqrtf(var + eps);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int c = j * 256 + lane * 8;
+      const int c = j * 256 + L * 8;
       const float4_t g0 = *reinterpret_cast<const float4_t*>(gamma + c);
       const float4_t g1 = *reinterpret_cast<const float4_t*>(gamma + c + 4);
       const float4_t b0 = *reinterpret_cast<const float4_t*>(beta + c);
@@ -110,36 +158,43 @@ __global__ __launch_bounds__(256) void rot_q8_1024_kernel(const half_t* __restri
           v[j * 8 + e] = a + b;
           v[(j + h) * 8 + e] = a - b;
         }
-  // column bits 3..7 (lane bits 0..4)
+  // column bits 3..7 (lanes)
+  const float s3 = gray_sign(L & 1), s4 = gray_sign(L & 2), s5 = gray_sign(L & 4), s6 = gray_sign(L & 8);
+  const float s7 = gray_sign(L & 16);
 #pragma unroll
-  for (int m = 1; m < 32; m <<= 1) {
-    const bool upper = lane & m;
+  for (int i = 0; i < 32; ++i) v[i] = bfly<DPP_XOR1>(v[i], s3);
 #pragma unroll
-    for (int i = 0; i < 32; ++i) v[i] = lane_butterfly(v[i], m, upper);
-  }
+  for (int i = 0; i < 32; ++i) v[i] = bfly<DPP_XOR3>(v[i], s4);
+#pragma unroll
+  for (int i = 0; i < 32; ++i) v[i] = bfly<DPP_XOR7>(v[i], s5);
+#pragma unroll
+  for (int i = 0; i < 32; ++i) v[i] = bfly<DPP_XOR15>(v[i], s6);
+#pragma unroll
+  for (int i = 0; i < 32; ++i) v[i] = __builtin_fmaf(swz_xor16(v[i]), s7, v[i]);
+  // v now holds (-1)^popcount(L) times the unnormalized rotation; x 1/32 is exact, so it joins the multiplier
   float amax = 0.f;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    v[i] = v[i] * 0.03125f;  // 1/sqrt(1024), exact
-    amax = fmaxf(amax, fabsf(v[i]));
-  }
-  amax = half_wave_max(amax);
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = half_wave_max(amax) * 0.03125f;
   const float scale = fmaxf(amax, 1e-12f) / 127.f;
   const float inv = 1.f / scale;
+  const float mul = (__builtin_popcount(L) & 1 ? -inv : inv) * 0.03125f;
   int8_t* orow = out + row * 1024;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     uint2 pk;
-    pk.x = q8x4(v[j * 8] * inv, v[j * 8 + 1] * inv, v[j * 8 + 2] * inv, v[j * 8 + 3] * inv);
-    pk.y = q8x4(v[j * 8 + 4] * inv, v[j * 8 + 5] * inv, v[j * 8 + 6] * inv, v[j * 8 + 7] * inv);
-    *reinterpret_cast<uint2*>(orow + j * 256 + lane * 8) = pk;
+    pk.x = pack4(v[j * 8] * mul, v[j * 8 + 1] * mul, v[j * 8 + 2] * mul, v[j * 8 + 3] * mul);
+    pk.y = pack4(v[j * 8 + 4] * mul, v[j * 8 + 5] * mul, v[j * 8 + 6] * mul, v[j * 8 + 7] * mul);
+    *reinterpret_cast<uint2*>(orow + j * 256 + L * 8) = pk;
   }
   if (lane == 0) row_scale[row] = scale;
 }
 
-// One row of C = 128*nb columns per 64-lane wave. Lane l = 16g + s owns, for i = 0..NI-1, the 8 columns
-// (4i + g)*128 + 8s + e of block 4i + g: column bits 0-2 in registers, bits 3-6 across the 16 lanes of a DPP row.
-// Stages run over column bits 0..6 in ascending order, as in kernels.cu:125-135. 4 rows per workgroup.
+// One row of C = 128*nb columns per 64-lane wave. Lane 16g + l owns, for i = 0..NI-1, the 8 columns
+// (4i + g)*128 + 8*gray(l) + e of block 4i + g: column bits 0-2 in registers, bits 3-6 across the 16 lanes of a DPP
+// row. Stages run over column bits 0..6 in ascending order, as in kernels.cu:125-135. 4 rows per workgroup.
+// LayerNorm (new; EVA02's norm after SwiGLU): gamma/beta are [C] with zeros past c_real; sums over the real columns
+// run per lane sequentially in (i, e) order, then over lanes by the xor tree 32, 16, 15, 7, 3, 1.
 template <int NI, bool NORM>
 __global__ __launch_bounds__(256) void rot_q8_h128_kernel(const half_t* __restrict__ x, int64_t T, int C, int c_real,
                                                           const float* __restrict__ gamma,
@@ -148,7 +203,7 @@ __global__ __launch_bounds__(256) void rot_q8_h128_kernel(const half_t* __restri
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= T) return;  // whole waves exit together
-  const int g = lane >> 4, s = lane & 15;
+  const int g = lane >> 4, l16 = lane & 15, gl = l16 ^ (l16 >> 1);
   const int nb = C >> 7;
   const half_t* xr = x + row * C;
   float v[NI * 8];
@@ -156,7 +211,7 @@ __global__ __launch_bounds__(256) void rot_q8_h128_kernel(const half_t* __restri
   for (int i = 0; i < NI; ++i) {
     const int b = 4 * i + g;
     if (b < nb) {
-      const half8_t h = *reinterpret_cast<const half8_t*>(xr + b * 128 + 8 * s);
+      const half8_t h = *reinterpret_cast<const half8_t*>(xr + b * 128 + 8 * gl);
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[i * 8 + e] = static_cast<float>(h[e]);
     } else {
@@ -165,13 +220,11 @@ __global__ __launch_bounds__(256) void rot_q8_h128_kernel(const half_t* __restri
     }
   }
   if constexpr (NORM) {
-    // LayerNorm over the first c_real columns; the rest are padding and stay zero. nreal[i] = how many of the
-    // lane's 8 columns of block 4i + g are real (the prefix e < nreal[i]).
-    int nreal[NI];
+    int nreal[NI];  // real columns among the lane's 8 of block 4i + g (a prefix)
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int b = 4 * i + g;
-      const int left = c_real - (b * 128 + 8 * s);
+      const int left = c_real - (b * 128 + 8 * gl);
       nreal[i] = b < nb ? (left < 0 ? 0 : (left > 8 ? 8 : left)) : 0;
     }
     float sum = 0.f;
@@ -179,8 +232,16 @@ __global__ __launch_bounds__(256) void rot_q8_h128_kernel(const half_t* __restri
     for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int e = 0; e < 8; ++e) sum = sum + (e < nreal[i] ? v[i * 8 + e] : 0.f);
+    auto tree = [](float t) {
+      t = t + xor_shuffle(t, 32);
+      t = t + swz_xor16(t);
+      t = t + dpp<DPP_XOR15>(t);
+      t = t + dpp<DPP_XOR7>(t);
+      t = t + dpp<DPP_XOR3>(t);
+      return t + dpp<DPP_XOR1>(t);
+    };
     const float fr = static_cast<float>(c_real);
-    const float mean = wave_sum(sum) / fr;
+    const float mean = tree(sum) / fr;
     float sq = 0.f;
 #pragma unroll
     for (int i = 0; i < NI; ++i)
@@ -190,36 +251,21 @@ __global__ __launch_bounds__(256) void rot_q8_h128_kernel(const half_t* __restri
         v[i * 8 + e] = d;
         sq = sq + d * d;
       }
-    const float var = wave_sum(sq) / fr;
+    const float var = tree(sq) / fr;
     const float rstd = 1.f / sqrtf(var + eps);
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const int col0 = (4 * i + g) * 128 + 8 * s;
-      float gg[8], bb[8];
-      if (nreal[i] == 8) {
-        const float4_t g0 = *reinterpret_cast<const float4_t*>(gamma + col0);
-        const float4_t g1 = *reinterpret_cast<const float4_t*>(gamma + col0 + 4);
-        const float4_t b0 = *reinterpret_cast<const float4_t*>(beta + col0);
-        const float4_t b1 = *reinterpret_cast<const float4_t*>(beta + col0 + 4);
+      const int b = 4 * i + g;
+      if (b >= nb) continue;  // lanes past the row end keep zeros (they take part in the row's absmax)
+      const int col0 = b * 128 + 8 * gl;  // gamma/beta are zero past c_real: no masking needed inside the row
+      const float4_t g0 = *reinterpret_cast<const float4_t*>(gamma + col0);
+      const float4_t g1 = *reinterpret_cast<const float4_t*>(gamma + col0 + 4);
+      const float4_t b0 = *reinterpret_cast<const float4_t*>(beta + col0);
+      const float4_t b1 = *reinterpret_cast<const float4_t*>(beta + col0 + 4);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          gg[e] = g0[e];
-          gg[e + 4] = g1[e];
-          bb[e] = b0[e];
-          bb[e + 4] = b1[e];
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int cc = e < nreal[i] ? col0 + e : 0;  // never read gamma/beta past c_real
-          gg[e] = gamma[cc];
-          bb[e] = beta[cc];
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float y = v[i * 8 + e] * rstd * gg[e] + bb[e];
-        v[i * 8 + e] = e < nreal[i] ? y : 0.f;
+      for (int e = 0; e < 4; ++e) {
+        v[i * 8 + e] = v[i * 8 + e] * rstd * g0[e] + b0[e];
+        v[i * 8 + 4 + e] = v[i * 8 + 4 + e] * rstd * g1[e] + b1[e];
       }
     }
   }
@@ -235,31 +281,37 @@ __global__ __launch_bounds__(256) void rot_q8_h128_kernel(const half_t* __restri
           v[i * 8 + e] = a + b;
           v[i * 8 + e + h] = a - b;
         }
-  // column bits 3..6 (lane bits 0..3)
+  // column bits 3..6 (lanes, Gray order)
+  const float s3 = gray_sign(gl & 1), s4 = gray_sign(gl & 2), s5 = gray_sign(gl & 4), s6 = gray_sign(gl & 8);
 #pragma unroll
-  for (int m = 1; m < 16; m <<= 1) {
-    const bool upper = lane & m;
+  for (int i = 0; i < NI * 8; ++i) v[i] = bfly<DPP_XOR1>(v[i], s3);
 #pragma unroll
-    for (int i = 0; i < NI * 8; ++i) v[i] = lane_butterfly(v[i], m, upper);
-  }
+  for (int i = 0; i < NI * 8; ++i) v[i] = bfly<DPP_XOR3>(v[i], s4);
+#pragma unroll
+  for (int i = 0; i < NI * 8; ++i) v[i] = bfly<DPP_XOR7>(v[i], s5);
+#pragma unroll
+  for (int i = 0; i < NI * 8; ++i) v[i] = bfly<DPP_XOR15>(v[i], s6);
+  // x fp32(1/sqrt(128)) is a rounded multiply (kernels.cu:138); rounding is sign-symmetric, so it may act on the
+  // sign-tracked values
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < NI * 8; ++i) {
-    v[i] = v[i] * 0.08838834764831845f;  // fp32(1/sqrt(128)), kernels.cu:138
+    v[i] = v[i] * 0.08838834764831845f;
     amax = fmaxf(amax, fabsf(v[i]));
   }
   amax = wave_max(amax);
   const float scale = fmaxf(amax, 1e-12f) / 127.f;
   const float inv = 1.f / scale;
+  const float mul = __builtin_popcount(gl) & 1 ? -inv : inv;
   int8_t* orow = out + row * C;
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int b = 4 * i + g;
     if (b < nb) {
       uint2 pk;
-      pk.x = q8x4(v[i * 8] * inv, v[i * 8 + 1] * inv, v[i * 8 + 2] * inv, v[i * 8 + 3] * inv);
-      pk.y = q8x4(v[i * 8 + 4] * inv, v[i * 8 + 5] * inv, v[i * 8 + 6] * inv, v[i * 8 + 7] * inv);
-      *reinterpret_cast<uint2*>(orow + b * 128 + 8 * s) = pk;
+      pk.x = pack4(v[i * 8] * mul, v[i * 8 + 1] * mul, v[i * 8 + 2] * mul, v[i * 8 + 3] * mul);
+      pk.y = pack4(v[i * 8 + 4] * mul, v[i * 8 + 5] * mul, v[i * 8 + 6] * mul, v[i * 8 + 7] * mul);
+      *reinterpret_cast<uint2*>(orow + b * 128 + 8 * gl) = pk;
     }
   }
   if (lane == 0) row_scale[row] = scale;

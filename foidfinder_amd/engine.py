@@ -24,7 +24,7 @@ from pathlib import Path
 import torch
 import torch.nn.functional as F
 
-from .kernels import EPI_QKV_ROPE, EPI_RESIDUAL, EPI_SWIGLU, kernels, lib
+from .kernels import EPI_QKV_ROPE, EPI_RESIDUAL, EPI_SWIGLU, kernels, lib, pad_norm
 
 Q_SCALE = 0.125 * math.log2(math.e)  # softmax scale x log2(e), folded into q by the QKV epilogue (engine.py:26)
 FORMAT = "foidfinder-eva02-int8-v1"
@@ -222,7 +222,7 @@ class Eva02Int8:
             {
                 "n1": norm(f"blocks.{i}.norm1"),
                 "n2": norm(f"blocks.{i}.norm2"),
-                "nm": norm(f"blocks.{i}.mlp.norm"),
+                "nm": pad_norm(*norm(f"blocks.{i}.mlp.norm"), cfg.hidden_pad),
                 "qkv": lin(f"blocks.{i}.attn.qkv"),
                 "proj": lin(f"blocks.{i}.attn.proj"),
                 "fc1": lin(f"blocks.{i}.mlp.fc1"),

@@ -116,7 +116,8 @@ def rot_q8_h128(
     eps: float = 1e-6,
 ) -> None:
     """x fp16 [T, C] (C % 128 == 0) -> out int8 [T, C], row_scale fp32 [T]; LayerNorm over the first c_real columns
-    (default: all) first if gamma is given."""
+    (default: all) first if gamma is given. gamma/beta are fp32 [C] with zeros in columns >= c_real
+    (`pad_norm` builds them)."""
     _on_gpu(x, out, row_scale, gamma, beta)
     _require(x.dim() == 2 and x.dtype == torch.float16, "x must be fp16 [T, C]")
     _require(out.dtype == torch.int8 and out.shape == x.shape, "out must be int8 [T, C]")
@@ -125,11 +126,20 @@ def rot_q8_h128(
     cr = c_real or C
     if gamma is not None:
         _require(beta is not None, "gamma and beta go together")
-        _require(gamma.dtype == beta.dtype == torch.float32 and gamma.numel() == beta.numel() == cr,
-                 "gamma/beta must be fp32 [c_real]")
+        _require(gamma.dtype == beta.dtype == torch.float32 and gamma.numel() == beta.numel() == C,
+                 "gamma/beta must be fp32 [C], zero past c_real")
     with torch.cuda.device(x.device):
         _check(lib().ff_rot_q8_h128(_ptr(x), x.size(0), C, cr, _ptr(gamma), _ptr(beta), eps, _ptr(out),
                                     _ptr(row_scale), _stream(x)))
+
+
+def pad_norm(weight: torch.Tensor, bias: torch.Tensor, C: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """LayerNorm gamma/beta over c_real columns -> fp32 [C] with zeros past c_real, as rot_q8_h128 takes them."""
+    g = torch.zeros(C, dtype=torch.float32, device=weight.device)
+    b = torch.zeros(C, dtype=torch.float32, device=weight.device)
+    g[: weight.numel()] = weight.float().reshape(-1)
+    b[: bias.numel()] = bias.float().reshape(-1)
+    return g, b
 
 
 def out_shape(M: int, N: int, epi: int) -> tuple[int, int]:

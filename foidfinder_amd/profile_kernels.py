@@ -15,7 +15,7 @@ import argparse
 import torch
 
 from .engine import Eva02Config, eva02_rope_tables
-from .kernels import EPI_QKV_ROPE, EPI_RESIDUAL, EPI_SWIGLU, kernels
+from .kernels import EPI_QKV_ROPE, EPI_RESIDUAL, EPI_SWIGLU, kernels, pad_norm
 
 COPY_BYTES = 1 << 30
 
@@ -54,7 +54,7 @@ def main() -> None:
     for _ in range(args.reps):
         k.rot_q8_1024(x, ones(d), zeros(d), a8, rs, cfg.eps)
         k.rot_q8_1024(o16, None, None, a8, rs, cfg.eps)
-        k.rot_q8_h128(h16, h8, rs, ones(h), zeros(h), h, cfg.eps)
+        k.rot_q8_h128(h16, h8, rs, *pad_norm(ones(h), zeros(h), hp), h, cfg.eps)
         k.gemm_s8(a8, w["qkv"], rs, cs["qkv"], zeros(3 * d), out_qkv, EPI_QKV_ROPE, 0, cos, sin, 0.18)
         k.gemm_s8(a8, w["proj"], rs, cs["proj"], zeros(d), xr, EPI_RESIDUAL, 0, None, None, 1.0)
         k.gemm_s8(a8, w["fc1"], rs, cs["fc1"], zeros(2 * hp), hout, EPI_SWIGLU, 0, None, None, 1.0)

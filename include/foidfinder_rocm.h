@@ -45,7 +45,8 @@ int ff_rot_q8_1024(const void* x, const float* gamma, const float* beta, float e
 
 /* Block-diagonal 128-point Walsh-Hadamard rotation + per-token int8 over rows of C (C % 128 == 0, C <= 6144).
  * x fp16 [T,C] -> out int8 [T,C], row_scale fp32 [T]. If gamma != NULL, LayerNorm over the first c_real columns
- * (gamma/beta fp32 [c_real], epsilon eps) is applied first and columns >= c_real are treated as zero padding.
+ * (epsilon eps) is applied first and columns >= c_real are treated as zero padding; gamma/beta are fp32 [C] with
+ * zeros in columns >= c_real.
  * Replaces op `rot_q8_h128(x, out!, row_scale!)`, foidfinder/backends/cuda/csrc/kernels.cu:238-251; the fused norm
  * is new (EVA02's SwiGLU LayerNorm, foidfinder/backends/mlx/kernels.py:31-72). */
 int ff_rot_q8_h128(const void* x, int64_t T, int64_t C, int64_t c_real, const float* gamma, const float* beta,

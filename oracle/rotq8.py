@@ -94,36 +94,37 @@ def layer_norm_h128(v: np.ndarray, c_real: int, gamma: np.ndarray, beta: np.ndar
     """LayerNorm over the first c_real of C columns (the rest are zero padding and stay zero).
 
     Reduction order of the HIP kernel that fuses this norm into the block-128 rotation (one 64-lane wave per row):
-    lane l = 16*g + s owns, for i = 0, 1, ..., columns (4i + g)*128 + 8s + e (e = 0..7) and sums the real ones
-    sequentially in (i, e) order; the 64 partial sums are combined by the xor tree 32, 16, 8, 4, 2, 1. mean =
-    sum / c_real and var = sumsq / c_real are IEEE divisions; rstd = 1 / sqrt(var + eps). No fused multiply-add.
-    (The reference has no such fused norm: its CUDA path is PixAI's GELU MLP. The op order follows the EVA02
-    SwiGLU + LayerNorm of foidfinder/backends/mlx/kernels.py:31-72.)"""
+    lane 16g + l owns, for i = 0, 1, ..., the columns (4i + g)*128 + 8*gray(l) + e (e = 0..7, gray(l) = l ^ (l >> 1))
+    and sums the real ones sequentially in (i, e) order; the 64 partial sums are combined by the xor tree over lanes
+    32, 16, 15, 7, 3, 1. mean = sum / c_real and var = sumsq / c_real are IEEE divisions; rstd = 1 / sqrt(var + eps).
+    No fused multiply-add. (The reference has no such fused norm: its CUDA path is PixAI's GELU MLP. The op order
+    follows the EVA02 SwiGLU + LayerNorm of foidfinder/backends/mlx/kernels.py:31-72.)"""
     T, C = v.shape
     nb = C // 128
     ni = (nb + 3) // 4
     real = np.arange(C) < c_real
-    # [T, lane(64), i*8 + e] -> column index and validity
-    cols = np.full((64, ni * 8), -1, np.int64)
+    cols = np.full((64, ni * 8), -1, np.int64)  # [lane, i*8 + e] -> column (-1: outside the row)
     for lane in range(64):
-        g, s = lane >> 4, lane & 15
+        g, l16 = lane >> 4, lane & 15
+        gl = l16 ^ (l16 >> 1)
         for i in range(ni):
             b = 4 * i + g
             if b < nb:
-                cols[lane, i * 8 : i * 8 + 8] = b * 128 + 8 * s + np.arange(8)
+                cols[lane, i * 8 : i * 8 + 8] = b * 128 + 8 * gl + np.arange(8)
     valid = (cols >= 0) & real[np.maximum(cols, 0)]
     safe = np.maximum(cols, 0)
     gathered = np.where(valid[None], v[:, safe], F32(0.0))  # [T, 64, ni*8]
     s = np.zeros((T, 64), F32)
     for k in range(ni * 8):
         s = s + gathered[:, :, k]
-    mean = _xor_tree(s, (32, 16, 8, 4, 2, 1)) / F32(c_real)
+    masks = (32, 16, 15, 7, 3, 1)
+    mean = _xor_tree(s, masks) / F32(c_real)
     d = np.where(real[None, :], v - mean[:, None], F32(0.0)).astype(F32)
     dg = np.where(valid[None], d[:, safe], F32(0.0))
     sq = np.zeros((T, 64), F32)
     for k in range(ni * 8):
         sq = sq + dg[:, :, k] * dg[:, :, k]
-    var = _xor_tree(sq, (32, 16, 8, 4, 2, 1)) / F32(c_real)
+    var = _xor_tree(sq, masks) / F32(c_real)
     rstd = F32(1.0) / np.sqrt(var + F32(eps))
     g_full = np.zeros(C, F32)
     b_full = np.zeros(C, F32)

@@ -91,8 +91,9 @@ def run_h128(x, dev, c_real=0, gamma=None, beta=None, eps=1e-6):
     xt = to_gpu(x, dev)
     out = torch.empty(x.shape, dtype=torch.int8, device=dev)
     rs = torch.empty(x.shape[0], dtype=torch.float32, device=dev)
-    g = None if gamma is None else to_gpu(gamma, dev)
-    b = None if beta is None else to_gpu(beta, dev)
+    g = b = None
+    if gamma is not None:
+        g, b = K.pad_norm(to_gpu(gamma, dev), to_gpu(beta, dev), x.shape[1])
     K.rot_q8_h128(xt, out, rs, g, b, c_real, eps)
     torch.cuda.synchronize()
     return out.cpu().numpy(), rs.cpu().numpy()
@@ -140,7 +141,7 @@ def run_gemm(dev, a, w, rs, cs, bias, epi, variant, out=None, rope=None, q_scale
 GEMM_SHAPES = [(1, 16, 64), (17, 48, 128), (300, 3072, 1024), (1025, 5632, 1024), (129, 1024, 2816), (257, 272, 192)]
 
 
-@pytest.mark.parametrize("variant", [1, 2])
+@pytest.mark.parametrize("variant", [1, 2, 3])
 @pytest.mark.parametrize(("M", "N", "K"), GEMM_SHAPES)
 def test_gemm_s8_int32_bit_exact(dev, rng, M, N, K, variant):
     a, w, rs, cs, bias = gemm_inputs(rng, M, N, K)
@@ -150,7 +151,7 @@ def test_gemm_s8_int32_bit_exact(dev, rng, M, N, K, variant):
     assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[:4].tolist()}: {got[tuple(bad[0])]} vs {want[tuple(bad[0])]}"
 
 
-@pytest.mark.parametrize("variant", [1, 2])
+@pytest.mark.parametrize("variant", [1, 2, 3])
 @pytest.mark.parametrize("epi", [OG.EPI_BIAS_F16, OG.EPI_RESIDUAL, OG.EPI_QKV_ROPE, OG.EPI_SWIGLU])
 def test_gemm_s8_epilogue_bit_exact(dev, rng, epi, variant):
     M, K = 1025, 1024
