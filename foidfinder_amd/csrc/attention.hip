@@ -1,167 +1,330 @@
 // Non-causal flash attention, head_dim 64, fp16 in / fp32 accumulate, on gfx950 fp16 MFMA.
 //
 // Input is the QKV GEMM's output: qkv fp16 [S*L, 3C] with q already rotated and scaled by softmax_scale*log2(e) and
-// k rotated, so the softmax is in base 2. One 256-thread workgroup = 4 waves x 32 queries of one (sequence, head).
-// K and V stream through LDS in 64-key tiles (double-buffered; V stored transposed so the PV product reads
-// contiguous keys). Each wave computes S^T = K Q^T with v_mfma_f32_32x32x16_f16, which leaves one query per lane
-// and 32 keys per lane-pair, so the online softmax (running max, exp2, running sum) stays in registers with a
-// single cross-lane exchange, and P^T feeds the PV MFMA (O^T = V^T P^T) directly as its column operand.
-// Tails: query rows >= L are computed but not stored; keys >= L are masked to -inf.
+// k rotated, so the softmax is in base 2. One 256-thread workgroup = 4 waves x 64 queries (two 32-query tiles per
+// wave, so each K/V fragment read from LDS serves 64 queries) of one (sequence, head).
 //
-// Reference: foidfinder/backends/cuda/csrc/attention.cuh:19-157 (which accumulates each 64-key block in fp16;
-// here every product and sum is fp32).
+// K and V stream through a 3-stage LDS ring of 64-key tiles filled by buffer loads straight into LDS
+// (buffer_load_dwordx4 ... lds: no VGPR staging, no LDS write instructions). The buffer descriptor of each tile ends
+// at the sequence's last row, so rows past L read as zeros without any address clamping. Both tiles are stored
+// row-major (64 keys x 128 B); K is read with ds_read_b128 and V with the transposing ds_read_b64_tr_b16, which
+// hands each lane 4 consecutive keys of one d column - the layout the PV MFMA wants - so V is never transposed in
+// software. Rows are XOR-swizzled in 16-byte chunks so that both read patterns are free of bank conflicts.
+//
+// Per wave and 32-query tile, S^T = K Q^T comes from v_mfma_f32_32x32x16_f16 with each lane holding one query and
+// 16 of every 32 keys (the other 16 sit in lane ^ 32), and P^T feeds the PV MFMA (O^T = V^T P^T) directly as its
+// column operand. The tile is processed in two 32-key halves (S, softmax, PV per half). At head_dim 64 the softmax,
+// not the MFMA, bounds the loop, so its common path is one exp2, half a convert and half a dot per score:
+//  * every S^T accumulator starts at -m_ref (the query's reference maximum, kept fp16-representable) through one
+//    extra MFMA whose operands hold 1 and -m_ref in a single k-slot; the first tile sets m_ref to its maximum;
+//  * p = v_exp_f32 (exp2), converted in pairs to fp16; each lane sums its fp16 p with fp32 dot2 (the same p that
+//    enter the PV product). While every lane's sum over a half stays <= SUM_LIMIT, every p <= SUM_LIMIT, which
+//    fp16 holds at full relative precision and fp32 accumulates far from overflow, so m_ref stays. Otherwise (rare:
+//    the scores rose well above m_ref) m_ref is raised to that half's maximum, O and l are rescaled by
+//    2^(m_old - m_new) and the half's p are recomputed.
+// Tails: query rows >= L are computed on clamped rows and not stored; keys >= L are masked to -inf.
+//
+// Reference: foidfinder/backends/cuda/csrc/attention.cuh:19-157 (which accumulates each 64-key block in fp16 and
+// rescales every block; here every product and sum is fp32).
+#include <type_traits>
+
 #include "common.h"
 
 namespace ff {
 
+typedef __attribute__((address_space(3))) void lds_void;
+
 constexpr int HD = 64;
-constexpr int BQ = 128;         // queries per workgroup
-constexpr int BKV = 64;         // keys per tile
-constexpr int VT_STRIDE = 68;   // halves per transposed-V row: 64 keys + 4 pad (136 B rows spread the banks)
+constexpr int QW = 64;                // queries per wave
+constexpr int BQ = 4 * QW;            // queries per workgroup
+constexpr int BKV = 64;               // keys per tile
+constexpr int STAGES = 3;             // LDS ring depth
+constexpr int TILE = BKV * HD;        // halves per K (or V) tile: 8 KB
+constexpr int LOADS = 4;              // buffer->LDS loads per thread per tile (2 for K, 2 for V)
+constexpr float SUM_LIMIT = 8192.f;   // per-lane half-tile sum of p above which m_ref is raised
+constexpr uint32_t RSRC_WORD3 = 0x00020000;  // buffer descriptor word 3: raw dword access (gfx9 family)
 
-// K tile rows of 128 B (8 chunks of 16 B), chunk XOR bits 1-3 of the row: the 16 lanes of one 16-byte LDS read pass
-// (64 banks, 256 B) read 16 rows -> 2 rows per 256-byte window, spread over 16 distinct slots.
-__device__ __forceinline__ int k_swz(int row, int chunk) { return row * HD + ((chunk ^ ((row >> 1) & 7)) << 3); }
+// Physical 16-byte slot of chunk c in row r. K rows are read 16 rows per ds_read_b128 pass: XOR with bits 1-3 of the
+// row spreads them over all 64 banks. V rows are read by the transposing b64 read, 4 rows x 64 B per 32-lane pass:
+// flipping the upper half of the row for rows 2, 3 (mod 4) keeps those 4 rows on distinct banks.
+__device__ __forceinline__ int k_slot(int r, int c) { return c ^ ((r >> 1) & 7); }
+__device__ __forceinline__ int v_slot(int r, int c) { return c ^ ((r & 2) << 1); }
 
-__global__ __launch_bounds__(256) void attention_kernel(const half_t* __restrict__ qkv, half_t* __restrict__ out,
-                                                        int L, int H) {
-  __shared__ __attribute__((aligned(16))) half_t sK[2][BKV * HD];
-  __shared__ __attribute__((aligned(16))) half_t sV[2][HD * VT_STRIDE];
+// ds_read_b64_tr_b16 as inline asm. The compiler's wait-insertion pass treats the builtin as possibly reading LDS
+// that in-flight buffer->LDS loads are writing and drains them all (s_waitcnt vmcnt(0)) before it, which would
+// serialize the LDS ring; this form is invisible to that pass. Ordering: "memory" keeps it after the barrier that
+// publishes the tile; the caller waits for the data (s_waitcnt lgkmcnt(0) tied to the result registers).
+template <int OFF>
+__device__ __forceinline__ void tr_read(half4_t& v, uint32_t lds_addr) {
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(lds_addr), "n"(OFF) : "memory");
+}
 
+__global__ __launch_bounds__(256, 2) void attention_kernel(const half_t* __restrict__ qkv, half_t* __restrict__ out,
+                                                           int L, int H) {
+  // K tile of ring slot st at smem + st*TILE, V tile at smem + (STAGES + st)*TILE
+  __shared__ __attribute__((aligned(1024))) half_t smem[2 * STAGES * TILE];
+
+  const uint32_t smem_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)smem));
   const int C = H * HD, ROW = 3 * C;
   // 1-D grid over (sequence, head, query block), query block fastest, remapped so that all query blocks of one
   // (sequence, head) run on one XCD and read its K and V through one L2.
   const int nq = (L + BQ - 1) / BQ;
   const int t = xcd_remap(blockIdx.x, gridDim.x);
   const int qb = t % nq, h = (t / nq) % H, seq = t / (nq * H);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 31, fh = lane >> 5;
   const int64_t tok0 = static_cast<int64_t>(seq) * L;
   const half_t* qbase = qkv + tok0 * ROW + h * HD;
   const half_t* kbase = qbase + C;
   const half_t* vbase = qbase + 2 * C;
 
-  // Q fragments (column operand of S^T): lane holds query q0 + fr, d = 16s + 8fh + 0..7.
-  const int q0 = qb * BQ + wave * 32;
-  const int qrow = min(q0 + fr, L - 1);
-  half8_t qf[4];
+  const int q0 = qb * BQ + wave * QW;
+  const bool active = q0 < L;  // a wave whose queries all lie past L only helps load K and V
+  // Q fragments (column operand of S^T): tile qt, lane holds query q0 + 32qt + fr, d = 16s + 8fh + 0..7.
+  half8_t qf[2][4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s)
-    qf[s] = *reinterpret_cast<const half8_t*>(qbase + static_cast<int64_t>(qrow) * ROW + 16 * s + 8 * fh);
+  for (int qt = 0; qt < 2; ++qt) {
+    const int qrow = min(q0 + 32 * qt + fr, L - 1);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      qf[qt][s] = *reinterpret_cast<const half8_t*>(qbase + static_cast<int64_t>(qrow) * ROW + 16 * s + 8 * fh);
+  }
+  // Consume Q here, so that the compiler's own wait for these loads is placed once, before the tile loop, and not
+  // inside it, where the same vmcnt counter also tracks the tile loads in flight.
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) asm volatile("" ::"v"(qf[qt][s]));
 
-  // Tile loads: 64 keys x 8 chunks of 8 halves for K and for V, two chunks of each per thread.
-  half8_t rk[2], rv[2];
-  auto gload = [&](int tile) {
+  // Tile loads: wave w fills the 1 KB blocks 2w and 2w + 1 of each tile (rows 8b .. 8b + 7); lane l writes LDS
+  // slot l of the block, so it fetches the chunk that the swizzle puts there.
+  uint32_t voff_k[2], voff_v[2];
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int idx = tid + 256 * p, key = min(tile * BKV + (idx >> 3), L - 1), c = idx & 7;
-      rk[p] = *reinterpret_cast<const half8_t*>(kbase + static_cast<int64_t>(key) * ROW + c * 8);
-      rv[p] = *reinterpret_cast<const half8_t*>(vbase + static_cast<int64_t>(key) * ROW + c * 8);
-    }
-  };
-  auto swrite = [&](int buf) {
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int idx = tid + 256 * p, key = idx >> 3, c = idx & 7;
-      *reinterpret_cast<half8_t*>(&sK[buf][k_swz(key, c)]) = rk[p];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) sV[buf][(c * 8 + i) * VT_STRIDE + key] = rv[p][i];
-    }
-  };
-
-  float16_t o[2];
-#pragma unroll
-  for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
-
+  for (int p = 0; p < 2; ++p) {
+    const int row = 8 * (2 * wave + p) + (lane >> 3), slot = lane & 7;
+    voff_k[p] = static_cast<uint32_t>((row * ROW + k_slot(row, slot) * 8) * 2);
+    voff_v[p] = static_cast<uint32_t>((row * ROW + v_slot(row, slot) * 8) * 2);
+  }
   const int ntiles = (L + BKV - 1) / BKV;
-  gload(0);
-  swrite(0);
-  __syncthreads();
-  for (int tile = 0; tile < ntiles; ++tile) {
-    const int cur = tile & 1;
-    if (tile + 1 < ntiles) gload(tile + 1);
-
-    // S^T[key][q] for the tile's two 32-key halves: lane holds q = q0 + fr and keys 8(r/4) + 4fh + r%4.
-    float16_t sc[2];
+  auto issue = [&](int tile) __attribute__((always_inline)) {
+    const int st = tile % STAGES;
+    const int64_t off = static_cast<int64_t>(tile) * BKV * ROW;
+    const int nrec = ((L - 1 - tile * BKV) * ROW + HD) * 2;  // bytes up to the end of the sequence's last row
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(kbase + off), 0, nrec, RSRC_WORD3);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(vbase + off), 0, nrec, RSRC_WORD3);
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sc[kt][r] = 0.f;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const half8_t kf = *reinterpret_cast<const half8_t*>(&sK[cur][k_swz(kt * 32 + fr, 2 * s + fh)]);
-        sc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], sc[kt], 0, 0, 0);
-      }
+    for (int p = 0; p < 2; ++p) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(smem + st * TILE + (2 * wave + p) * 512), 16,
+                                               voff_k[p], 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(smem + (STAGES + st) * TILE + (2 * wave + p) * 512),
+                                               16, voff_v[p], 0, 0, 0);
     }
-    if (tile == ntiles - 1) {  // mask keys past the sequence end
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = tile * BKV + kt * 32 + 8 * (r >> 2) + 4 * fh + (r & 3);
-          if (key >= L) sc[kt][r] = -INFINITY;
-        }
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[kt][r]);
-    mx = fmaxf(mx, xor_shuffle(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float corr = exp2f(m_run - m_new);
-    m_run = m_new;
-    half8_t pf[2][2];
-    float psum = 0.f;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = exp2f(sc[kt][r] - m_new);
-        psum += p;
-        pf[kt][r >> 3][r & 7] = static_cast<half_t>(p);
-      }
-    l_run = l_run * corr + psum;
-#pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[dt][r] *= corr;
+  };
 
-    // O^T[d][q] += V^T[d][keys] P^T[keys][q]. MFMA slot u of lane half fh is key 16t + 8(u/4) + 4fh + u%4 of the
-    // 32-key half kt, both for the P^T registers (S^T rows 8t..8t+7) and for the V^T reads below.
+  // LDS read offsets (halves, within a tile). K fragment (kh, s): row kh*32 + fr, chunk 2s + fh. V^T fragment
+  // (dt, kh, tt), half j: the transposing read over 16-lane groups; lane l of group g addresses row
+  // kh*32 + 16tt + 8j + 4fh + (l%16)/4, columns dt*32 + 16(g%2) + 4(l%4) .. +3, and receives 4 consecutive keys of
+  // column dt*32 + fr: MFMA slots 4j .. 4j+3 = keys 16tt + 8j + 4fh + 0..3, the keys of P^T's slots.
+  int koff[4], voff[2];
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
+  for (int s = 0; s < 4; ++s) koff[s] = fr * HD + k_slot(fr, 2 * s + fh) * 8;
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const half_t* vr = &sV[cur][(dt * 32 + fr) * VT_STRIDE + kt * 32 + 16 * t + 4 * fh];
-          const half4_t lo = *reinterpret_cast<const half4_t*>(vr);
-          const half4_t hi = *reinterpret_cast<const half4_t*>(vr + 8);
-          const half8_t vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[kt][t], o[dt], 0, 0, 0);
-        }
-    if (tile + 1 < ntiles) swrite(cur ^ 1);
-    __syncthreads();
+  for (int dt = 0; dt < 2; ++dt) {
+    const int row = 4 * fh + ((lane & 15) >> 2);  // + kh*32 + 16tt + 8j, multiples of 4 that leave row & 2 alone
+    const int col = dt * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    voff[dt] = row * HD + v_slot(row, col >> 3) * 8 + (col & 7);
   }
 
-  const float l_tot = l_run + xor_shuffle(l_run, 32);
-  const float inv = 1.f / l_tot;
-  const int q = q0 + fr;
-  if (q < L) {
-    half_t* orow = out + (tok0 + q) * C + h * HD;
+  float16_t o[2][2];  // [query tile][d tile]: O^T rows d = 32dt + 8(r/4) + 4fh + r%4, column = the lane's query
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        half4_t v;
+      for (int r = 0; r < 16; ++r) o[qt][dt][r] = 0.f;
+  // m_ref enters S through one extra MFMA per accumulator: the row operand `one_k` has 1 in k-slot 0 for every key,
+  // the column operand mq[qt] holds -m_ref (fp16) of the lane's query in k-slot 0, so the product starts every
+  // S^T accumulator at -m_ref without a register block per query tile. m_ref is kept fp16-representable.
+  half8_t one_k = {}, mq[2] = {{}, {}};
+  if (fh == 0) one_k[0] = static_cast<half_t>(1.f);
+  float m_ref[2] = {0.f, 0.f}, l_run[2] = {0.f, 0.f};
+  const half2_t ones = {static_cast<half_t>(1.f), static_cast<half_t>(1.f)};
+  auto set_mref = [&](int qt, float m) __attribute__((always_inline)) {
+    // smallest fp16 >= m (|m| < 65504): then every p of the tile that set it is <= 1
+    const float mc = fminf(fmaxf(m, -65000.f), 65000.f);
+    half_t mh = static_cast<half_t>(mc + fabsf(mc) * 0.0009765625f + 6.103515625e-05f);
+    m_ref[qt] = static_cast<float>(mh);
+    if (fh == 0) mq[qt][0] = -mh;
+  };
+
+  // Per tile, the two 32-key halves kh are pipelined: S of half 1 is computed (MFMA) while the softmax of half 0
+  // runs (VALU), and the PV product of half 0 while the softmax of half 1 runs.
+  float16_t xs[2][2];    // [kh][qt]: S^T - m_ref, lane holds keys 32kh + 8(r/4) + 4fh + r%4
+  half8_t pf[2][2][2];   // [kh][qt][tt]: fp16 p, slot u of lane half fh = key 32kh + 16tt + 8(u/4) + 4fh + u%4
+  float hs[2][2];        // [kh][qt]: the lane's sum of its p over half kh
+  int ka[4], va[2];      // this tile's K and V read bases
+
+  auto qk = [&](int kh, int tile, bool last) __attribute__((always_inline)) {
+    const float16_t zero = {};
 #pragma unroll
-        for (int t = 0; t < 4; ++t) v[t] = static_cast<half_t>(o[dt][4 * g + t] * inv);
-        *reinterpret_cast<half4_t*>(orow + dt * 32 + 8 * g + 4 * fh) = v;
+    for (int qt = 0; qt < 2; ++qt) xs[kh][qt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(one_k, mq[qt], zero, 0, 0, 0);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const half8_t kf = *reinterpret_cast<const half8_t*>(smem + ka[s] + kh * 32 * HD);
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt)
+        xs[kh][qt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[qt][s], xs[kh][qt], 0, 0, 0);
+    }
+    if (last) {  // keys past the sequence end (their K rows read as zeros)
+      // opaque, so that the 16 comparisons are not hoisted out of the tile loop as 16 live lane masks
+      int lim = L - tile * BKV - kh * 32 - 4 * fh;
+      asm volatile("" : "+v"(lim));
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        if (8 * (r >> 2) + (r & 3) >= lim) {
+          xs[kh][0][r] = -INFINITY;
+          xs[kh][1][r] = -INFINITY;
+        }
       }
+    }
+  };
+  auto soft = [&](int kh) __attribute__((always_inline)) {
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      float acc = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const half2_t p2 = {static_cast<half_t>(__builtin_amdgcn_exp2f(xs[kh][qt][r])),
+                            static_cast<half_t>(__builtin_amdgcn_exp2f(xs[kh][qt][r + 1]))};
+        acc = __builtin_amdgcn_fdot2(p2, ones, acc, false);
+        pf[kh][qt][r >> 3][r & 7] = p2[0];
+        pf[kh][qt][r >> 3][(r & 7) + 1] = p2[1];
+      }
+      hs[kh][qt] = acc;
+    }
+  };
+  auto pv = [&](auto khc) __attribute__((always_inline)) {
+    constexpr int kh = decltype(khc)::value;
+    half4_t v[2][2][2];  // [dt][tt][j]
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      const uint32_t base = smem_lds + 2u * static_cast<uint32_t>(va[dt]);
+      tr_read<(kh * 32 + 0) * HD * 2>(v[dt][0][0], base);
+      tr_read<(kh * 32 + 8) * HD * 2>(v[dt][0][1], base);
+      tr_read<(kh * 32 + 16) * HD * 2>(v[dt][1][0], base);
+      tr_read<(kh * 32 + 24) * HD * 2>(v[dt][1][1], base);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[0][0][0]), "+v"(v[0][0][1]), "+v"(v[0][1][0]), "+v"(v[0][1][1]), "+v"(v[1][0][0]),
+                   "+v"(v[1][0][1]), "+v"(v[1][1][0]), "+v"(v[1][1][1]));
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const half4_t lo = v[dt][tt][0], hi = v[dt][tt][1];
+        const half8_t vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt)
+          o[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[kh][qt][tt], o[qt][dt], 0, 0, 0);
+      }
+  };
+  // Lane-pair maximum of xs[kh][qt] (the query's 32 keys of half kh).
+  auto half_max = [&](int kh, int qt) __attribute__((always_inline)) {
+    float v = xs[kh][qt][0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) v = fmaxf(v, xs[kh][qt][r]);
+    return fmaxf(v, xor_shuffle(v, 32));
+  };
+  // Rare path of a half whose p overflowed the limit: raise m_ref to the maximum of S over that half (S recomputed
+  // under the old m_ref), rescale O, l and the sum of half 0 when rescuing half 1, and recompute the S halves whose
+  // softmax is still to come under the new m_ref.
+  auto rescue = [&](int kh, int tile, bool last) __attribute__((always_inline)) {
+    qk(kh, tile, last);
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const float m_old = m_ref[qt];
+      const float mx = half_max(kh, qt) + m_old;
+      if (mx > m_old) set_mref(qt, mx);
+      const float corr = __builtin_amdgcn_exp2f(m_old - m_ref[qt]);
+      l_run[qt] *= corr;
+      if (kh == 1) hs[0][qt] *= corr;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[qt][dt][r] *= corr;
+    }
+    qk(kh, tile, last);
+    soft(kh);
+  };
+
+#pragma unroll
+  for (int j = 0; j < STAGES - 1; ++j)
+    if (j < ntiles) issue(j);
+  for (int tile = 0; tile < ntiles; ++tile) {
+    // Tile `tile` has landed once at most the loads of the tiles issued after it are outstanding.
+    if (tile + 1 < ntiles)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LOADS * (STAGES - 2)) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // no fence: the vmcnt wait above already covers this thread's LDS writes
+    // The ring slot of tile + STAGES - 1 was last read for tile - 1, which every wave has finished.
+    if (tile + STAGES - 1 < ntiles) issue(tile + STAGES - 1);
+    if (!active) continue;
+    // Read bases, opaque to the compiler so that the fragment offsets fold into the reads' immediate offsets
+    // instead of each being precomputed into a register.
+    const int st = tile % STAGES;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      ka[s] = st * TILE + koff[s];
+      asm volatile("" : "+v"(ka[s]));
+    }
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      va[dt] = (STAGES + st) * TILE + voff[dt];
+      asm volatile("" : "+v"(va[dt]));
+    }
+    // One tile (a single copy of the code: per-variant copies of the MFMA regions make the register allocator
+    // shuffle the accumulators between them). Each half's p are checked (all lane sums <= SUM_LIMIT) before its PV
+    // product; the first tile sets m_ref from its maximum first.
+    const bool last = tile == ntiles - 1;
+    qk(0, tile, last);
+    if (tile == 0) {
+      qk(1, tile, last);
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) set_mref(qt, fmaxf(half_max(0, qt), half_max(1, qt)));
+      qk(0, tile, last);
+    }
+    soft(0);
+    if (__any(hs[0][0] > SUM_LIMIT || hs[0][1] > SUM_LIMIT)) rescue(0, tile, last);
+    pv(std::integral_constant<int, 0>{});
+    qk(1, tile, last);
+    soft(1);
+    if (__any(hs[1][0] > SUM_LIMIT || hs[1][1] > SUM_LIMIT)) rescue(1, tile, last);
+    pv(std::integral_constant<int, 1>{});
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) l_run[qt] += hs[0][qt] + hs[1][qt];
+  }
+
+  if (!active) return;
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const float l_tot = l_run[qt] + xor_shuffle(l_run[qt], 32);
+    const float inv = 1.f / l_tot;
+    const int q = q0 + 32 * qt + fr;
+    if (q < L) {
+      half_t* orow = out + (tok0 + q) * C + h * HD;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          half4_t v;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) v[u] = static_cast<half_t>(o[qt][dt][4 * g + u] * inv);
+          *reinterpret_cast<half4_t*>(orow + dt * 32 + 8 * g + 4 * fh) = v;
+        }
+    }
   }
 }
 
@@ -174,7 +337,8 @@ extern "C" int ff_attention(const void* qkv, void* out, int64_t T, int64_t heads
   if (heads <= 0 || heads > 65535) return fail(FF_EINVAL, "attention: need 0 < heads <= 65535");
   if (seq_len <= 0 || seq_len > 0x7fffffff) return fail(FF_EINVAL, "attention: need seq_len > 0");
   if (T < 0 || T % seq_len != 0) return fail(FF_EINVAL, "attention: T must be a multiple of seq_len");
-  if (heads * 3 * HD * seq_len > (int64_t(1) << 40)) return fail(FF_EINVAL, "attention: too large");
+  // K/V tiles are addressed by 32-bit byte offsets within one sequence
+  if (seq_len * heads * 3 * HD * 2 >= (int64_t(1) << 31)) return fail(FF_EINVAL, "attention: sequence too large");
   const int64_t seqs = T / seq_len;
   if (T == 0) return FF_OK;
   if (!qkv || !out) return fail(FF_EINVAL, "attention: null pointer");

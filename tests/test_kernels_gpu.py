@@ -205,6 +205,22 @@ def test_attention_matches_float64(dev, rng, S, L, H):
     assert np.isfinite(got).all() and err < 4e-3, f"max abs err {err}"
 
 
+@pytest.mark.parametrize(("gain", "ramp"), [(8.0, 3.0), (30.0, 0.0), (4.0, 12.0)])
+def test_attention_peaked_and_rising_scores(dev, rng, gain, ramp):
+    """Scores of tens to hundreds (base 2) whose maxima grow along the keys: the running maximum must be raised on
+    later key tiles, not only set on the first one."""
+    S, L, H = 2, 1025, 4
+    qkv = qkv_inputs(rng, S, L, H).astype(np.float32)
+    qkv[:, : H * 64] *= np.float32(gain)
+    pos = np.tile(np.arange(L, dtype=np.float32), S)
+    qkv[:, H * 64 : 2 * H * 64] *= (1.0 + ramp * pos / L)[:, None]
+    qkv = qkv.astype(np.float16)
+    got = run_attention(dev, qkv, L).astype(np.float64)
+    want = OA.attention(qkv, L, out_dtype=np.float64)
+    err = np.abs(got - want).max()
+    assert np.isfinite(got).all() and err < 4e-3, f"max abs err {err}"
+
+
 def test_attention_identical_keys_give_mean_of_values(dev, rng):
     S, L, H = 1, 200, 4
     qkv = qkv_inputs(rng, S, L, H)
