@@ -1,8 +1,9 @@
 // W8A8 GEMM with exact int32 accumulation on gfx950 int8 MFMA, and the fused fp16 epilogues.
 //
 // acc[m, n] = sum_k A[m, k] W[n, k]; A [M, K] and W [N, K] are int8 with K contiguous.
-// y = ((float)acc * row_scale[m]) * col_scale[n] + bias[n] (three roundings; this file is built with
-// -ffp-contract=off), then the epilogue. The integer part is exact, so the order of the k-sum is free: each lane
+// y = fma((float)acc * row_scale[m], col_scale[n], bias[n]) - the reference's `acc * rs * cs + bias` as its CUDA
+// compiler contracts it (gemm.cuh:135-136; this file is built with -ffp-contract=off, so every other operation rounds
+// separately) - then the epilogue. The integer part is exact, so the order of the k-sum is free: each lane
 // feeds the MFMA 16 contiguous bytes of K and the A- and W-fragments use the same k slots.
 //
 // Both kernels use 256-thread workgroups (4 waves as 2 x 2), 64-byte K slices in LDS with the 16-byte chunks of
@@ -47,25 +48,14 @@ constexpr int BK = 64;
 // where XOR with bits 1-2 doubles every read).
 __device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ ((row >> 2) & 3)) << 4); }
 
-// exp(x) from plain fp32 operations in a fixed order (no fused multiply-add: this file is built with
-// -ffp-contract=off), so the CPU oracle reproduces it bit for bit: Cody-Waite range reduction x = n ln2 + r with ln2
-// split into a 16-bit head and a tail (n * head is exact for |n| < 256), a degree-6 Taylor polynomial for e^r on
-// |r| <= ln2/2, then an exact scaling by 2^n; relative error below 3e-7 over [-80, 80].
-__device__ __forceinline__ float exp_cw(float x) {
-  const float n = __builtin_rintf(x * 1.44269504088896341f);
-  const float r = (x - n * 0.693145751953125f) - n * 1.428606765330187045e-06f;
-  float p = 1.f / 720.f;
-  p = p * r + 1.f / 120.f;
-  p = p * r + 1.f / 24.f;
-  p = p * r + 1.f / 6.f;
-  p = p * r + 0.5f;
-  p = p * r + 1.f;
-  p = p * r + 1.f;
-  const int e = static_cast<int>(fminf(fmaxf(n, -300.f), 300.f));
-  return ldexpf(p, e);
+// silu(g) = g / (1 + e^-g) from the hardware transcendental units: e^-g = v_exp_f32(-g log2 e) and the quotient as
+// g * v_rcp_f32(1 + e^-g), each about 1 ulp, so silu(g) * value lands within one fp16 ulp of the correctly rounded
+// result (the reference's own exp is a platform library call, mlx/kernels.py:45-49). Limits: g -> -inf gives
+// e^-g = inf, rcp = 0, silu = -0; g -> +inf gives g.
+__device__ __forceinline__ float silu(float g) {
+  const float e = __builtin_amdgcn_exp2f(-g * 1.44269504088896341f);
+  return g * __builtin_amdgcn_rcpf(1.f + e);
 }
-
-__device__ __forceinline__ float silu(float g) { return g / (1.f + exp_cw(-g)); }
 
 __device__ __forceinline__ float gelu_tanh(float y) {
   return 0.5f * y * (1.f + tanhf(0.7978845608f * (y + 0.044715f * y * y * y)));
@@ -120,22 +110,37 @@ __device__ __forceinline__ void store_epilogue(const int16_t_v (&acc)[NI][MI], i
     const int out_n0 = SWI ? n_base / 2 : n_base;
     const int C3 = N / 3;  // QKV: section width
     half_t* o16 = static_cast<half_t*>(args.out);
+    // Scale and bias of the wave's 32 NI columns, loaded once per lane column group (i, q) (clamped past N: those
+    // columns are never stored).
+    float4_t cs[NI][4], bi[NI][4];
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = min(n_base + 32 * i + 8 * q + 4 * fk, N - 4);
+        cs[i][q] = *reinterpret_cast<const float4_t*>(args.col_scale + n);
+        bi[i][q] = *reinterpret_cast<const float4_t*>(args.bias + n);
+      }
 #pragma unroll
     for (int j = 0; j < MI; ++j) {
       const int mrow = m_base + 32 * j + fr;
       const int m = min(mrow, M - 1);  // rows past M are computed on clamped inputs and never stored
       const float rs = args.row_scale[m];
+      const float* rcos = nullptr;
+      const float* rsin = nullptr;
+      if constexpr (EPI == FF_EPI_QKV_ROPE) {
+        rcos = args.rope_cos + (m % args.rope_len) * 32;
+        rsin = args.rope_sin + (m % args.rope_len) * 32;
+      }
 #pragma unroll
       for (int i = 0; i < NI; ++i)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int c = 32 * i + 8 * q + 4 * fk;  // column within the wave's tile
-          const int n = min(n_base + c, N - 4);   // past-N columns: clamped reads, never stored
-          const float4_t cs = *reinterpret_cast<const float4_t*>(args.col_scale + n);
-          const float4_t bi = *reinterpret_cast<const float4_t*>(args.bias + n);
           float y[4];
 #pragma unroll
-          for (int t = 0; t < 4; ++t) y[t] = static_cast<float>(acc[i][j][4 * q + t]) * rs * cs[t] + bi[t];
+          for (int t = 0; t < 4; ++t)
+            y[t] = __builtin_fmaf(static_cast<float>(acc[i][j][4 * q + t]) * rs, cs[i][q][t], bi[i][q][t]);
           if constexpr (SWI) {
             half2_t h;
             h[0] = static_cast<half_t>(silu(y[0]) * y[1]);
@@ -143,15 +148,19 @@ __device__ __forceinline__ void store_epilogue(const int16_t_v (&acc)[NI][MI], i
             *reinterpret_cast<half2_t*>(stage + fr * RB + c) = h;  // output column c/2, 2 bytes each
           } else {
             if constexpr (EPI == FF_EPI_QKV_ROPE) {
+              const int n = n_base + c;
               const int section = n / C3;
               if (section < 2) {
-                const int trow = (m % args.rope_len) * 32 + ((n & 63) >> 1);
+                // the two pairs (n, n+1), (n+2, n+3) use table entries (n mod 64)/2 and the next one
+                const int pi = (n & 63) >> 1;
+                const float2 co = *reinterpret_cast<const float2*>(rcos + pi);
+                const float2 si = *reinterpret_cast<const float2*>(rsin + pi);
+                const float qs = section == 0 ? args.q_scale : 1.f;
+                const float c2[2] = {co.x, co.y}, s2[2] = {si.x, si.y};
 #pragma unroll
                 for (int pr = 0; pr < 2; ++pr) {
-                  const float co = args.rope_cos[trow + pr], si = args.rope_sin[trow + pr];
                   const float y0 = y[2 * pr], y1 = y[2 * pr + 1];
-                  const float r0 = y0 * co - y1 * si, r1 = y0 * si + y1 * co;
-                  const float qs = section == 0 ? args.q_scale : 1.f;
+                  const float r0 = y0 * c2[pr] - y1 * s2[pr], r1 = y0 * s2[pr] + y1 * c2[pr];
                   y[2 * pr] = section == 0 ? r0 * qs : r0;
                   y[2 * pr + 1] = section == 0 ? r1 * qs : r1;
                 }
@@ -163,7 +172,13 @@ __device__ __forceinline__ void store_epilogue(const int16_t_v (&acc)[NI][MI], i
             }
             half4_t h;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) h[t] = static_cast<half_t>(y[t]);
+            for (int t = 0; t < 4; ++t) {
+              // y is rounded to fp32 first, then to fp16: opaque here, so the compiler cannot fold the last fma and
+              // the conversion into one v_fma_mix (a single rounding straight to fp16, which differs in ~3e-5 of
+              // the outputs from the two-step rounding of the reference)
+              asm("" : "+v"(y[t]));
+              h[t] = static_cast<half_t>(y[t]);
+            }
             *reinterpret_cast<half4_t*>(stage + fr * RB + 2 * c) = h;
           }
         }
@@ -321,6 +336,361 @@ __global__ __launch_bounds__(256, 1) void gemm_s8_pipe_kernel(const GemmArgs arg
                               smem + wave * stage_bytes<EPI, NI>());
 }
 
+// ---------------- variant 4: 256 x 128 tiles, 3-stage buffer->LDS ring, 2 workgroups per CU ----------------
+//
+// Sized for gfx950's feeds: an L2->CU load rate of ~55 B/clk per CU against 8192 int8 ops/clk per CU asks for
+// >= ~150 ops per loaded byte (a 256 x 128 tile gives 171), and each wave's 128 x 64 sub-tile needs 96 B/clk of the
+// ~240 B/clk LDS read rate. 72 KB of LDS and <= 256 registers per lane let two workgroups share a CU, so one
+// workgroup's epilogue runs while the other's MFMAs do. Loads are buffer loads straight into LDS whose descriptors
+// end at row M (or N): rows past the matrix read as zeros and need no clamping, and the per-slice offset lives in
+// the scalar descriptor, so the main loop spends no VALU on addresses.
+
+constexpr int R_BM = 256, R_BN = 128;
+constexpr int R_GROUP_M = 8;                 // m-tiles per tile group
+constexpr uint32_t RSRC_WORD3 = 0x00020000;  // buffer descriptor word 3: raw dword access (gfx9 family)
+
+// LDS row layout of a K slice of RK bytes (64: 4 chunks of 16 B, 32: 2 chunks). A 16-byte-per-lane read pass covers
+// 16 rows and 64 banks: with 64-byte rows the chunk XOR bits 2-3 of the row spreads rows r, r+4, r+8, r+12; with
+// 32-byte rows (8 rows per 256 B) the chunk XOR bit 3 of the row separates r from r+8.
+template <int RK>
+__device__ __forceinline__ int rswz(int row, int chunk) {
+  if constexpr (RK == 64)
+    return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4);
+  else
+    return row * 32 + ((chunk ^ ((row >> 3) & 1)) << 4);
+}
+
+// One 16-byte-per-lane buffer load into LDS through a raw descriptor of `nbytes` bytes at `base` (loads past it read
+// zeros). A plain function, so the descriptor type never appears in a template-dependent expression: the host pass
+// of HIP cannot instantiate those and would silently drop the kernel's launch stub.
+__device__ __forceinline__ void buffer_to_lds(const void* base, int nbytes, uint8_t* lds_dst, uint32_t voff) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nbytes, RSRC_WORD3);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds_dst, 16, voff, 0, 0, 0);
+}
+
+// RK: K bytes per ring slot (64 or 32), S: ring depth. The prefetch distance is S - 2 slots (plus half a slot for
+// RK = 64), so RK = 32 with 6 slots doubles it in the same 72 KB.
+template <int EPI, int RK, int S>
+__global__ __launch_bounds__(256, 2) void gemm_s8_ring_kernel(const GemmArgs args) {
+  constexpr int WM = R_BM / 2, WN = R_BN / 2, MI = WM / 32, NI = WN / 32;
+  constexpr int STAGE = (R_BM + R_BN) * RK;      // bytes per ring slot (24 KB or 12 KB)
+  constexpr int LOADS = STAGE / (256 * 16);      // 16-byte loads per thread per slot (6 or 3)
+  constexpr int A_BLOCKS = R_BM * RK / 1024;     // 1 KB blocks of A per slot; W blocks follow
+  constexpr int CPR = RK / 16;                   // 16-byte chunks per row
+  constexpr int HALVES = RK / 32;                // 32-byte MFMA k-steps per slot
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[S * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tiles_m = (args.M + R_BM - 1) / R_BM, tiles_n = (args.N + R_BN - 1) / R_BN;
+  const int t = xcd_remap(blockIdx.x, gridDim.x);
+  const int per_group = R_GROUP_M * tiles_n;
+  const int g = t / per_group, in_g = t % per_group;
+  const int gm = min(R_GROUP_M, tiles_m - g * R_GROUP_M);
+  const int tm = g * R_GROUP_M + in_g % gm, tn = in_g / gm;
+  const int m0 = tm * R_BM, n0 = tn * R_BN;
+  const int K = args.K, KT = K / RK;
+
+  // Slot layout: A_BLOCKS blocks of 1 KB (A rows) then the W blocks. Wave w issues blocks w*LOADS .. +LOADS-1; lane
+  // l of a block writes LDS bytes 16 l, i.e. row l / CPR, slot l % CPR, and fetches the chunk rswz() puts there.
+  uint32_t voff[LOADS];
+#pragma unroll
+  for (int p = 0; p < LOADS; ++p) {
+    const int blk = wave * LOADS + p;
+    const int brow = (blk < A_BLOCKS ? blk : blk - A_BLOCKS) * (1024 / RK);
+    const int row = brow + lane / CPR, slot = lane % CPR;
+    voff[p] = static_cast<uint32_t>(row * K + ((rswz<RK>(row, slot) - row * RK)));
+  }
+  // descriptor sizes: the bytes from the tile's first row to the end of the matrix (capped; in-tile offsets are
+  // below 256 K, far under the cap)
+  const int64_t a_rows = static_cast<int64_t>(args.M - m0) * K, w_rows = static_cast<int64_t>(args.N - n0) * K;
+  auto nrec = [](int64_t bytes) { return static_cast<int>(bytes < 0x7fffffff ? bytes : 0x7fffffff); };
+  auto issue = [&](int kt) __attribute__((always_inline)) {
+    uint8_t* st = smem + (kt % S) * STAGE;
+    const int kb = kt * RK;
+    const int8_t* abase = args.A + static_cast<int64_t>(m0) * K + kb;
+    const int8_t* wbase = args.W + static_cast<int64_t>(n0) * K + kb;
+    const int an = nrec(a_rows - kb), wn_ = nrec(w_rows - kb);
+#pragma unroll
+    for (int p = 0; p < LOADS; ++p) {
+      const int blk = wave * LOADS + p;  // wave-uniform
+      if (blk < A_BLOCKS)
+        buffer_to_lds(abase, an, st + blk * 1024, voff[p]);
+      else
+        buffer_to_lds(wbase, wn_, st + blk * 1024, voff[p]);
+    }
+  };
+
+  int16_t_v acc[NI][MI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+#pragma unroll
+    for (int j = 0; j < MI; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < KT) issue(s);
+
+  const int fr = lane & 31, fk = lane >> 5;
+  int4_t xw0[NI], ya0[MI], xw1[NI], ya1[MI];
+  // fragments of 32-byte k-step kk of slot kt
+  auto read_frags = [&](int kt, int kk, int4_t (&xw)[NI], int4_t (&ya)[MI]) __attribute__((always_inline)) {
+    const uint8_t* sa = smem + (kt % S) * STAGE;
+    const uint8_t* sw = sa + R_BM * RK;
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      xw[i] = *reinterpret_cast<const int4_t*>(sw + rswz<RK>(wn * WN + i * 32 + fr, 2 * kk + fk));
+#pragma unroll
+    for (int j = 0; j < MI; ++j)
+      ya[j] = *reinterpret_cast<const int4_t*>(sa + rswz<RK>(wm * WM + j * 32 + fr, 2 * kk + fk));
+  };
+  auto mfmas = [&](const int4_t (&xw)[NI], const int4_t (&ya)[MI]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int j = 0; j < MI; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xw[i], ya[j], acc[i][j], 0, 0, 0);
+  };
+  auto interleave = [] __attribute__((always_inline)) {
+#pragma unroll
+    for (int x = 0; x < NI + MI; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NI * MI - (NI + MI), 0);
+  };
+  // Slot kt + 1 has landed once at most the loads of the newer slots are outstanding; lgkmcnt(0): this thread's
+  // fragment reads of older slots are complete, so after the barrier any of them may be refilled.
+  auto wait_next = [&](auto steady) __attribute__((always_inline)) {
+    if constexpr (decltype(steady)::value)
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((S - 2) * LOADS) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+  };
+
+  if (KT >= S - 1)
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((S - 2) * LOADS) : "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  read_frags(0, 0, xw0, ya0);
+
+  // One slot per step. STEADY: slot kt + S - 1 exists and is issued into the ring position of slot kt - 1, whose
+  // fragments every wave finished reading before the previous barrier. With RK = 64 the second k-step of slot kt is
+  // read while the first one's MFMAs run, and the first k-step of slot kt + 1 (after its barrier) while the second
+  // one's run; with RK = 32, slot kt + 1 is read while slot kt's MFMAs run. On the last slot the read-ahead hits a
+  // stale ring position and is never used.
+  auto step = [&](int kt, auto steady) __attribute__((always_inline)) {
+    if constexpr (decltype(steady)::value) issue(kt + S - 1);
+    if constexpr (HALVES == 2) {
+      read_frags(kt, 1, xw1, ya1);
+      mfmas(xw0, ya0);
+      interleave();
+      wait_next(steady);
+      read_frags(kt + 1, 0, xw0, ya0);
+      mfmas(xw1, ya1);
+      interleave();
+    } else {
+      wait_next(steady);
+      read_frags(kt + 1, 0, xw1, ya1);
+      mfmas(xw0, ya0);
+      interleave();
+#pragma unroll
+      for (int i = 0; i < NI; ++i) xw0[i] = xw1[i];
+#pragma unroll
+      for (int j = 0; j < MI; ++j) ya0[j] = ya1[j];
+    }
+  };
+  int kt = 0;
+  for (; kt + S - 1 < KT; ++kt) step(kt, std::true_type{});
+  for (; kt < KT; ++kt) step(kt, std::false_type{});
+  __syncthreads();  // every wave is done with the ring; reuse it as the epilogue staging area
+  static_assert(4 * stage_bytes<FF_EPI_QKV_ROPE, NI>() <= S * STAGE, "staging must fit in the ring");
+  store_epilogue<EPI, NI, MI>(acc, m0 + wm * WM, n0 + wn * WN, lane, args, smem + wave * stage_bytes<EPI, NI>());
+}
+
+template <int RK, int S>
+static int launch_ring(const GemmArgs& a, int epi, hipStream_t st) {
+  if (a.K % RK != 0) return fail(FF_EINVAL, "gemm_s8: K must be a multiple of the slice");
+  const int64_t tiles = static_cast<int64_t>((a.M + R_BM - 1) / R_BM) * ((a.N + R_BN - 1) / R_BN);
+  if (tiles > 0x7fffffff) return fail(FF_EINVAL, "gemm_s8: too many tiles");
+  const dim3 grid(static_cast<unsigned>(tiles));
+  switch (epi) {
+    case FF_EPI_QKV_ROPE: gemm_s8_ring_kernel<FF_EPI_QKV_ROPE, RK, S><<<grid, 256, 0, st>>>(a); break;
+    case FF_EPI_RESIDUAL: gemm_s8_ring_kernel<FF_EPI_RESIDUAL, RK, S><<<grid, 256, 0, st>>>(a); break;
+    case FF_EPI_GELU_F16: gemm_s8_ring_kernel<FF_EPI_GELU_F16, RK, S><<<grid, 256, 0, st>>>(a); break;
+    case FF_EPI_SWIGLU: gemm_s8_ring_kernel<FF_EPI_SWIGLU, RK, S><<<grid, 256, 0, st>>>(a); break;
+    case FF_EPI_BIAS_F16: gemm_s8_ring_kernel<FF_EPI_BIAS_F16, RK, S><<<grid, 256, 0, st>>>(a); break;
+    case FF_EPI_I32: gemm_s8_ring_kernel<FF_EPI_I32, RK, S><<<grid, 256, 0, st>>>(a); break;
+    default: return fail(FF_EINVAL, "gemm_s8: bad epilogue");
+  }
+  return check_launch("gemm_s8");
+}
+
+// ---------------- variants 6, 7: 256 x 256 tiles, 8 waves, buffer->LDS ring ----------------
+//
+// Halves the load traffic per MFMA of the 256 x 128 ring (the CU's vector-memory path, not the MFMA, bounds that
+// kernel): 8 waves (2 per SIMD, each a 128 x 64 sub-tile as before) share one 256 x 256 tile, one workgroup per CU
+// with a 128 KB ring. RK = 128 reads whole 128-byte lines per row and slot (2 slots); RK = 64 keeps 4 slots.
+
+template <int RK>
+__device__ __forceinline__ int wswz(int row, int chunk) {
+  if constexpr (RK == 128)
+    return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4);  // 8 rows per read pass window pair: rows r, r+2, ...
+  else
+    return rswz<RK>(row, chunk);
+}
+
+template <int EPI, int RK, int S>
+__global__ __launch_bounds__(512, 1) void gemm_s8_wide_kernel(const GemmArgs args) {
+  constexpr int BM = 256, BN = 256, WM = 128, WN = 64, MI = WM / 32, NI = WN / 32;
+  constexpr int STAGE = (BM + BN) * RK;       // bytes per ring slot (64 KB or 32 KB)
+  constexpr int LOADS = STAGE / (512 * 16);   // 16-byte loads per thread per slot (8 or 4)
+  constexpr int A_BLOCKS = BM * RK / 1024;    // 1 KB blocks of A per slot; W blocks follow
+  constexpr int CPR = RK / 16;                // 16-byte chunks per row
+  constexpr int KSTEPS = RK / 32;             // 32-byte MFMA k-steps per slot
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[S * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2, wn = wave & 3;
+  const int tiles_m = (args.M + BM - 1) / BM, tiles_n = (args.N + BN - 1) / BN;
+  const int t = xcd_remap(blockIdx.x, gridDim.x);
+  const int per_group = R_GROUP_M * tiles_n;
+  const int g = t / per_group, in_g = t % per_group;
+  const int gm = min(R_GROUP_M, tiles_m - g * R_GROUP_M);
+  const int tm = g * R_GROUP_M + in_g % gm, tn = in_g / gm;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int K = args.K, KT = K / RK;
+
+  uint32_t voff[LOADS];
+#pragma unroll
+  for (int p = 0; p < LOADS; ++p) {
+    const int blk = wave * LOADS + p;
+    const int brow = (blk < A_BLOCKS ? blk : blk - A_BLOCKS) * (1024 / RK);
+    const int row = brow + lane / CPR, slot = lane % CPR;
+    voff[p] = static_cast<uint32_t>(row * K + ((wswz<RK>(row, slot) - row * RK)));
+  }
+  const int64_t a_rows = static_cast<int64_t>(args.M - m0) * K, w_rows = static_cast<int64_t>(args.N - n0) * K;
+  auto nrec = [](int64_t bytes) { return static_cast<int>(bytes < 0x7fffffff ? bytes : 0x7fffffff); };
+  auto issue = [&](int kt) __attribute__((always_inline)) {
+    uint8_t* st = smem + (kt % S) * STAGE;
+    const int kb = kt * RK;
+    const int8_t* abase = args.A + static_cast<int64_t>(m0) * K + kb;
+    const int8_t* wbase = args.W + static_cast<int64_t>(n0) * K + kb;
+    const int an = nrec(a_rows - kb), wn_ = nrec(w_rows - kb);
+#pragma unroll
+    for (int p = 0; p < LOADS; ++p) {
+      const int blk = wave * LOADS + p;  // wave-uniform
+      if (blk < A_BLOCKS)
+        buffer_to_lds(abase, an, st + blk * 1024, voff[p]);
+      else
+        buffer_to_lds(wbase, wn_, st + blk * 1024, voff[p]);
+    }
+  };
+
+  int16_t_v acc[NI][MI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+#pragma unroll
+    for (int j = 0; j < MI; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < KT) issue(s);
+
+  const int fr = lane & 31, fk = lane >> 5;
+  int4_t xw[2][NI], ya[2][MI];
+  auto read_frags = [&](int kt, int kk, int b) __attribute__((always_inline)) {
+    const uint8_t* sa = smem + (kt % S) * STAGE;
+    const uint8_t* sw = sa + BM * RK;
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      xw[b][i] = *reinterpret_cast<const int4_t*>(sw + wswz<RK>(wn * WN + i * 32 + fr, 2 * kk + fk));
+#pragma unroll
+    for (int j = 0; j < MI; ++j)
+      ya[b][j] = *reinterpret_cast<const int4_t*>(sa + wswz<RK>(wm * WM + j * 32 + fr, 2 * kk + fk));
+  };
+  auto mfmas = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < MI; ++j)
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xw[b][i], ya[b][j], acc[i][j], 0, 0, 0);
+  };
+  auto interleave = [] __attribute__((always_inline)) {
+#pragma unroll
+    for (int x = 0; x < NI + MI; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NI * MI - (NI + MI), 0);
+  };
+  auto wait_next = [&](auto steady) __attribute__((always_inline)) {
+    if constexpr (decltype(steady)::value)
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((S - 2) * LOADS) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+  };
+
+  if (KT >= S - 1)
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((S - 2) * LOADS) : "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  read_frags(0, 0, 0);
+
+  // One slot per step: the k-steps of slot kt are computed in order, each while the next one's fragments are read;
+  // before the last k-step, slot kt + 1 is waited for (and the barrier passed), so its first k-step is read while
+  // slot kt's last one computes. STEADY: slot kt + S - 1 is issued first, into the ring position of slot kt - 1.
+  auto step = [&](int kt, auto steady) __attribute__((always_inline)) {
+    if constexpr (decltype(steady)::value) issue(kt + S - 1);
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+      const int b = kk & 1;
+      if (kk + 1 < KSTEPS) {
+        read_frags(kt, kk + 1, b ^ 1);
+      } else {
+        wait_next(steady);
+        read_frags(kt + 1, 0, b ^ 1);
+      }
+      mfmas(b);
+      interleave();
+    }
+  };
+  int kt = 0;
+  for (; kt + S - 1 < KT; ++kt) step(kt, std::true_type{});
+  for (; kt < KT; ++kt) step(kt, std::false_type{});
+  __syncthreads();  // every wave is done with the ring; reuse it as the epilogue staging area
+  static_assert(8 * stage_bytes<FF_EPI_QKV_ROPE, NI>() <= S * STAGE, "staging must fit in the ring");
+  store_epilogue<EPI, NI, MI>(acc, m0 + wm * WM, n0 + wn * WN, lane, args, smem + wave * stage_bytes<EPI, NI>());
+}
+
+template <int RK, int S>
+static int launch_wide(const GemmArgs& a, int epi, hipStream_t st) {
+  if (a.K % RK != 0) return fail(FF_EINVAL, "gemm_s8: K must be a multiple of the slice");
+  const int64_t tiles = static_cast<int64_t>((a.M + 255) / 256) * ((a.N + 255) / 256);
+  if (tiles > 0x7fffffff) return fail(FF_EINVAL, "gemm_s8: too many tiles");
+  const dim3 grid(static_cast<unsigned>(tiles));
+  switch (epi) {
+    case FF_EPI_QKV_ROPE: gemm_s8_wide_kernel<FF_EPI_QKV_ROPE, RK, S><<<grid, 512, 0, st>>>(a); break;
+    case FF_EPI_RESIDUAL: gemm_s8_wide_kernel<FF_EPI_RESIDUAL, RK, S><<<grid, 512, 0, st>>>(a); break;
+    case FF_EPI_GELU_F16: gemm_s8_wide_kernel<FF_EPI_GELU_F16, RK, S><<<grid, 512, 0, st>>>(a); break;
+    case FF_EPI_SWIGLU: gemm_s8_wide_kernel<FF_EPI_SWIGLU, RK, S><<<grid, 512, 0, st>>>(a); break;
+    case FF_EPI_BIAS_F16: gemm_s8_wide_kernel<FF_EPI_BIAS_F16, RK, S><<<grid, 512, 0, st>>>(a); break;
+    case FF_EPI_I32: gemm_s8_wide_kernel<FF_EPI_I32, RK, S><<<grid, 512, 0, st>>>(a); break;
+    default: return fail(FF_EINVAL, "gemm_s8: bad epilogue");
+  }
+  return check_launch("gemm_s8");
+}
+
 // ---------------- variants 2, 3: register-staged double buffering ----------------
 
 template <int BM, int BN, int EPI>
@@ -448,8 +818,11 @@ static int launch_pipe(const GemmArgs& a, int epi, hipStream_t st) {
   return check_launch("gemm_s8");
 }
 
-// 1: 256 x 256 pipelined (direct-to-LDS, 4 stages); 2: 128 x 128 staged; 3: 256 x 128 staged.
-constexpr int kVariants = 3;
+// 1: 256 x 256 pipelined (direct-to-LDS, 4 stages); 2: 128 x 128 staged; 3: 256 x 128 staged;
+// 4, 5: 256 x 128 buffer->LDS ring, two workgroups per CU (3 slots of K 64, 6 slots of K 32);
+// 6, 7: 256 x 256, 8 waves, one workgroup per CU (2 slots of K 128 - or variant 7 when K % 128 != 0 -, 4 slots
+// of K 64).
+constexpr int kVariants = 7;
 
 }  // namespace ff
 
@@ -473,6 +846,7 @@ extern "C" int ff_gemm_s8(const int8_t* A, const int8_t* W, int64_t M, int64_t N
   if (epi == FF_EPI_QKV_ROPE) {
     if (N % 3 != 0 || (N / 3) % 64 != 0) return fail(FF_EINVAL, "gemm_s8: QKV epilogue needs N = 3C with C % 64 == 0");
     if (!rope_cos || !rope_sin || rope_len <= 0) return fail(FF_EINVAL, "gemm_s8: QKV epilogue needs RoPE tables");
+    if (!aligned(rope_cos, 8) || !aligned(rope_sin, 8)) return fail(FF_EINVAL, "gemm_s8: misaligned RoPE tables");
   }
   if (M == 0) return FF_OK;
   if (!A || !W || !out) return fail(FF_EINVAL, "gemm_s8: null pointer");
@@ -501,6 +875,10 @@ extern "C" int ff_gemm_s8(const int8_t* A, const int8_t* W, int64_t M, int64_t N
     case 1: return launch_pipe(a, epi, st);
     case 2: return launch_staged<128, 128>(a, epi, st);
     case 3: return launch_staged<256, 128>(a, epi, st);
+    case 4: return launch_ring<64, 3>(a, epi, st);
+    case 5: return launch_ring<32, 6>(a, epi, st);
+    case 6: return a.K % 128 == 0 ? launch_wide<128, 2>(a, epi, st) : launch_wide<64, 4>(a, epi, st);
+    case 7: return launch_wide<64, 4>(a, epi, st);
   }
   return fail(FF_EINVAL, "gemm_s8: bad variant");
 }

@@ -296,7 +296,7 @@ class Eva02Int8:
 
     def _forward(self, img: torch.Tensor, buf: dict[str, torch.Tensor], trace: dict | None = None) -> torch.Tensor:
         """One forward into the preallocated buffers. `trace` (eager debugging only) collects copies of the stem
-        output and, per block, the qkv, attention output and block output."""
+        output and, per block, the qkv, attention output, SwiGLU output and block output."""
         k, cfg = self.k, self.cfg
         B, L, d = img.shape[0], cfg.tokens, cfg.dim
         x, a8, rs = buf["x"], buf["a8"], buf["rs"]
@@ -318,6 +318,8 @@ class Eva02Int8:
             self._gemm(a8, lw["proj"], rs, EPI_RESIDUAL, v["proj"], x)
             k.rot_q8_1024(x, *lw["n2"], a8, rs, eps)
             self._gemm(a8, lw["fc1"], rs, EPI_SWIGLU, v["fc1"], buf["h16"])
+            if trace is not None:
+                trace[f"h{i}"] = buf["h16"].clone()
             k.rot_q8_h128(buf["h16"], buf["h8"], rs, *lw["nm"], cfg.hidden, eps)
             self._gemm(buf["h8"], lw["fc2"], rs, EPI_RESIDUAL, v["fc2"], x)
             if trace is not None:

@@ -25,6 +25,10 @@ PINNED = {
     "RNE ties; LayerNorm variant vs float64 LayerNorm",
     "rotq8.rot_q8_h128": "block-diagonal H128 closed form; padded columns stay zero; LN over real columns only",
     "gemm.gemm_s8_i32": "exact: int64 brute force on small shapes, float64 BLAS bound |acc| < 2^53",
+    "gemm.fma32": "equals exact rational arithmetic rounded once (random operands); a constructed halfway case "
+    "where a tiny addend decides the rounding (a float64-then-float32 computation gets it wrong)",
+    "gemm.dequant": "each element equals the rational (acc*rs) * cs + bias rounded once",
+    "gemm.exp_cw": "relative error below 3e-7 against float64 exp over [-80, 80]",
     "gemm.epilogue": "closed forms: RoPE at cls row is the identity, pair rotation preserves norm, SwiGLU of "
     "zero-padded columns is zero, residual adds in fp16",
     "attention.attention": "identical keys -> mean of V; one dominant logit -> that V row; shift invariance",

@@ -1,7 +1,8 @@
 """W8A8 GEMM with exact int32 accumulation and the fused fp16 epilogues, restated in numpy.
 
 acc[m, n] = sum_k A[m, k] * W[n, k] (int8 x int8 -> int32, exact), then
-y = ((float(acc) * row_scale[m]) * col_scale[n]) + bias[n]       (three float32 roundings, no fused multiply-add)
+y = fma(float(acc) * row_scale[m], col_scale[n], bias[n])   (one rounding for the product, one for the fused step:
+    the reference's `acc * rs * cs + bias` as the CUDA compiler contracts it, gemm.cuh:135-136)
 and per epilogue (reference: foidfinder/backends/cuda/csrc/gemm.cuh:119-171, Epi enum gemm.cuh:8-12):
 
   QKV_ROPE  interleaved-pair rotation on the q and k sections (n < 2C, C = N/3) with table row m % rope_len and pair
@@ -9,7 +10,9 @@ and per epilogue (reference: foidfinder/backends/cuda/csrc/gemm.cuh:119-171, Epi
             q additionally x q_scale; fp16 out                                              (gemm.cuh:140-151)
   RESIDUAL  x <- fp16(fp16(y) + x)                                                         (gemm.cuh:163-169)
   GELU_F16  fp16(gelu_tanh(y))                                                  (gemm.cuh:137-139, common.cuh:50-56)
-  SWIGLU    columns interleaved as (gate j, value j) pairs: h[j] = fp16(silu(y[2j]) * y[2j+1]), out [M, N/2]
+  SWIGLU    columns interleaved as (gate j, value j) pairs: h[j] = fp16(silu(y[2j]) * y[2j+1]), out [M, N/2];
+            silu uses exp_cw below, a deterministic exp (the GPU uses its ~1-ulp transcendental units and lands within
+            one fp16 ulp of this)
             (no CUDA counterpart; EVA02 SwiGLU of foidfinder/backends/mlx/kernels.py:45-49 with the gate-first fc1
             rows of foidfinder/haruka.py:59-60 interleaved at conversion)
   BIAS_F16  fp16(y)
@@ -33,11 +36,32 @@ def gemm_s8_i32(a: np.ndarray, w: np.ndarray) -> np.ndarray:
     return acc.astype(np.int64).astype(np.int32)
 
 
+def fma32(a: np.ndarray, b: np.ndarray, c: np.ndarray) -> np.ndarray:
+    """Correctly rounded float32 a * b + c with a single rounding (the hardware's fused multiply-add).
+
+    a * b is exact in float64 (24 + 24 significant bits); Knuth's TwoSum splits p + c exactly into s + e in float64.
+    Rounding s to float32 is then the correct rounding of p + c unless s lies exactly halfway between two float32
+    values and e != 0: the sign of e then decides (numpy's tie-to-even would ignore it)."""
+    a, b, c = np.broadcast_arrays(np.asarray(a, F32), np.asarray(b, F32), np.asarray(c, F32))
+    p = a.astype(np.float64) * b.astype(np.float64)
+    c64 = c.astype(np.float64)
+    s = p + c64
+    bb = s - p
+    e = (p - (s - bb)) + (c64 - bb)
+    r = s.astype(F32)
+    d = s - r.astype(np.float64)  # exact: r is the float32 rounding of s
+    toward = np.where(d > 0, F32(np.inf), F32(-np.inf)).astype(F32)
+    other = np.nextafter(r, toward)  # the float32 neighbour on s's side of r
+    with np.errstate(invalid="ignore", over="ignore"):
+        mid = (r.astype(np.float64) + other.astype(np.float64)) * 0.5
+    fix = (d != 0) & (s == mid) & (e != 0) & ((e > 0) == (d > 0))
+    return np.where(fix, other, r).astype(F32)
+
+
 def dequant(acc: np.ndarray, row_scale: np.ndarray, col_scale: np.ndarray, bias: np.ndarray) -> np.ndarray:
-    """y = ((float(acc) * rs[m]) * cs[n]) + bias[n] in float32 (gemm.cuh:135-136 without the FMA contraction)."""
-    y = acc.astype(F32) * row_scale.astype(F32)[:, None]
-    y = y * col_scale.astype(F32)[None, :]
-    return y + bias.astype(F32)[None, :]
+    """y = fma(float(acc) * rs[m], cs[n], bias[n]) in float32 (gemm.cuh:135-136 as contracted by its compiler)."""
+    t = acc.astype(F32) * row_scale.astype(F32)[:, None]
+    return fma32(t, col_scale.astype(F32)[None, :], bias.astype(F32)[None, :])
 
 
 def gelu_tanh(y: np.ndarray) -> np.ndarray:

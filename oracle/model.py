@@ -248,12 +248,14 @@ def block_int8(
     rope: tuple[np.ndarray, np.ndarray],
     *,
     attention_out: np.ndarray | None = None,
+    hidden_out: np.ndarray | None = None,
     record: dict | None = None,
 ):
     """One int8 block on the fp16 residual stream x [B*L, d] -> new x.
 
-    attention_out, if given, replaces the attention output (teacher forcing: every other op is then a pure function
-    of its inputs, so a kernel implementation must reproduce the block bit for bit); record collects qkv and o."""
+    attention_out and hidden_out, if given, replace the attention output and the SwiGLU output (teacher forcing at
+    the two floating-point ops whose GPU results are not bit-reproducible: every other op is then a pure function of
+    its inputs, so a kernel implementation must reproduce the block bit for bit); record collects qkv, o and h."""
     cos, sin = rope
     a8, rs = rotq8.rot_q8_1024(x, qb["norm1_w"], qb["norm1_b"], cfg.eps)
     qkv = G.gemm_s8(
@@ -267,6 +269,10 @@ def block_int8(
     x = G.gemm_s8(a8, qb["proj.qweight"], rs, qb["proj.wscale"], qb["proj.bias"], G.EPI_RESIDUAL, residual=x)
     a8, rs = rotq8.rot_q8_1024(x, qb["norm2_w"], qb["norm2_b"], cfg.eps)
     h = G.gemm_s8(a8, qb["fc1.qweight"], rs, qb["fc1.wscale"], qb["fc1.bias"], G.EPI_SWIGLU)
+    if record is not None:
+        record["h"] = h
+    if hidden_out is not None:
+        h = hidden_out
     h8, rs = rotq8.rot_q8_h128(h, cfg.hidden, qb["mlp_norm_w"], qb["mlp_norm_b"], cfg.eps)
     return G.gemm_s8(h8, qb["fc2.qweight"], rs, qb["fc2.wscale"], qb["fc2.bias"], G.EPI_RESIDUAL, residual=x)
 

@@ -73,7 +73,11 @@ def check_wiring(eng, state, cfg, images, dev):
     for i, qb in enumerate(blocks):
         rec = {}
         o_eng = trace[f"attn{i}"].cpu().numpy()
-        x_new = OM.block_int8(x, qb, ocfg, rope, attention_out=o_eng, record=rec)
+        h_eng = trace[f"h{i}"].cpu().numpy()
+        x_new = OM.block_int8(x, qb, ocfg, rope, attention_out=o_eng, hidden_out=h_eng, record=rec)
+        h_want = rec["h"].astype(np.float32)
+        ulp = np.maximum(np.spacing(np.abs(rec["h"])), np.spacing(np.abs(h_eng))).astype(np.float32)
+        assert (np.abs(h_eng.astype(np.float32) - h_want) <= ulp).all(), f"block {i}: SwiGLU output beyond one ulp"
         qkv_eng = trace[f"qkv{i}"].cpu().numpy()
         assert np.array_equal(rec["qkv"].view(np.uint16), qkv_eng.view(np.uint16)), f"block {i}: qkv differs"
         x_eng = trace[f"x{i}"].cpu().numpy()

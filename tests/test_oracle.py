@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import itertools
 import math
+from fractions import Fraction
 
 import numpy as np
 import pytest
@@ -183,6 +184,56 @@ def test_dequant_matches_float64(rng):
     got = OG.dequant(acc, rs, cs, b)
     want = acc.astype(np.float64) * rs[:, None] * cs[None, :] + b[None, :]
     assert np.abs(got - want).max() <= 4 * np.finfo(F32).eps * np.abs(want).max()
+
+
+def _round_f32(x: Fraction) -> np.float32:
+    """Correct round-to-nearest-even of a rational to float32 (normal and subnormal range), by integer arithmetic."""
+    if x == 0:
+        return F32(0.0)
+    sign, x = (-1 if x < 0 else 1), abs(x)
+    e = x.numerator.bit_length() - x.denominator.bit_length()
+    while Fraction(2) ** e > x:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= x:
+        e += 1
+    e = max(e, -126)
+    q = x / Fraction(2) ** (e - 23)
+    n = q.numerator // q.denominator
+    rem = q - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return F32(sign * n * 2.0 ** (e - 23))
+
+
+def test_fma32_is_single_rounding(rng):
+    n = 3000
+    a = (rng.standard_normal(n) * rng.choice([1e-3, 1.0, 1e3], n)).astype(F32)
+    b = rng.standard_normal(n).astype(F32)
+    c = (rng.standard_normal(n) * rng.choice([1e-6, 1.0, 1e4], n)).astype(F32)
+    got = OG.fma32(a, b, c)
+    want = np.array([_round_f32(Fraction(float(x)) * Fraction(float(y)) + Fraction(float(z))) for x, y, z in zip(a, b, c)])
+    assert np.array_equal(got.view(np.uint32), want.astype(F32).view(np.uint32))
+
+
+def test_fma32_breaks_ties_by_the_addend():
+    """(1 + 2^-12)^2 = 1 + 2^-11 + 2^-24 is halfway between two float32 values: a tiny addend must decide the rounding
+    (a float64 sum rounded to float32 rounds twice and ties to even, the planted mistake this guards against)."""
+    x = np.array([1 + 2.0**-12], F32)
+    up, down = F32(1 + 2.0**-11 + 2.0**-23), F32(1 + 2.0**-11)
+    assert OG.fma32(x, x, np.array([2.0**-60], F32))[0] == up
+    assert OG.fma32(x, x, np.array([-(2.0**-60)], F32))[0] == down
+    assert OG.fma32(x, x, np.array([0.0], F32))[0] == down  # exact tie: to even
+    assert F32(np.float64(x[0]) * np.float64(x[0]) + 2.0**-60) == down  # the double-rounded value is wrong
+
+
+def test_dequant_is_fused(rng):
+    acc = rng.integers(-2**20, 2**20, (4, 8)).astype(np.int32)
+    rs, cs, b = rng.random(4).astype(F32), rng.random(8).astype(F32), rng.standard_normal(8).astype(F32)
+    got = OG.dequant(acc, rs, cs, b)
+    t = acc.astype(F32) * rs[:, None]
+    for m in range(4):
+        for n in range(8):
+            assert got[m, n] == _round_f32(Fraction(float(t[m, n])) * Fraction(float(cs[n])) + Fraction(float(b[n])))
 
 
 def test_qkv_rope_epilogue_closed_forms(rng):
