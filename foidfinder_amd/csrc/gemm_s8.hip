@@ -61,10 +61,12 @@ __device__ __forceinline__ float gelu_tanh(float y) {
   return 0.5f * y * (1.f + tanhf(0.7978845608f * (y + 0.044715f * y * y * y)));
 }
 
-// Per-wave LDS staging area of store_epilogue: 32 rows of the wave's output columns, each row padded by 8 bytes so
-// the 8-byte writes of 32 lanes (32 rows, one column group) and the 16-byte row reads both hit 64 distinct banks.
+// Per-wave LDS staging area of store_epilogue: 32 rows of the wave's output columns, each row padded so that the
+// writes of 32 lanes (32 rows, one column group) and the 16-byte row reads both spread over the 64 banks. fp16 rows
+// (8-byte pad), except QKV, which stages the fp32 y (16-byte pad) and applies RoPE after the transpose to rows.
 template <int EPI, int NI>
 constexpr int stage_row_bytes() {
+  if constexpr (EPI == FF_EPI_QKV_ROPE) return NI * 32 * 4 + 16;
   return (EPI == FF_EPI_SWIGLU ? NI * 16 : NI * 32) * 2 + 8;
 }
 template <int EPI, int NI>
@@ -74,9 +76,11 @@ constexpr int stage_bytes() {
 
 // The epilogue of one wave: acc[i][j][4q + t] is D[n][m] with m = m_base + 32j + (lane & 31) and
 // n = n_base + 32i + 8q + 4*(lane >> 5) + t. For each 32-row block j the wave computes y and the fp16 results in
-// registers (pairs of columns are in-lane for RoPE and SwiGLU), writes them to its LDS staging area, and then stores
-// whole 16-byte row segments (for RESIDUAL: loads the matching residual segment and adds in fp16), so global stores
-// are row-contiguous instead of 16 bytes per row. `stage` is this wave's private area of stage_bytes<EPI, NI>().
+// registers (pairs of columns are in-lane for SwiGLU), writes them to its LDS staging area, and then stores whole
+// 16-byte row segments (for RESIDUAL: loads the matching residual segment and adds in fp16), so global stores are
+// row-contiguous instead of 16 bytes per row. QKV stages y itself and rotates in the row layout, where the 8 lanes
+// of a row read that row's RoPE table entries as 16-byte runs instead of 32 scattered rows per load. `stage` is this
+// wave's private area of stage_bytes<EPI, NI>().
 template <int EPI, int NI, int MI>
 __device__ __forceinline__ void store_epilogue(const int16_t_v (&acc)[NI][MI], int m_base, int n_base, int lane,
                                                const GemmArgs& args, uint8_t* stage) {
@@ -117,21 +121,54 @@ __device__ __forceinline__ void store_epilogue(const int16_t_v (&acc)[NI][MI], i
     for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int n = min(n_base + 32 * i + 8 * q + 4 * fk, N - 4);
-        cs[i][q] = *reinterpret_cast<const float4_t*>(args.col_scale + n);
-        bi[i][q] = *reinterpret_cast<const float4_t*>(args.bias + n);
+        const int nc = min(n_base + 32 * i + 8 * q + 4 * fk, N - 4);
+        cs[i][q] = *reinterpret_cast<const float4_t*>(args.col_scale + nc);
+        bi[i][q] = *reinterpret_cast<const float4_t*>(args.bias + nc);
       }
+    // Per-row inputs are software-pipelined: the row scale of block j + 1 is loaded as soon as block j's results are
+    // computed, and the residual rows (or RoPE table rows) of block j + 1 as soon as block j is stored, so their
+    // latency hides behind the other phase. The staging area needs no barrier: one wave's LDS operations execute in
+    // order.
+    float rs = 0.f;
+    half8_t xres[32 / ROWS_PER_PASS];
+    float4_t tco[32 / ROWS_PER_PASS], tsi[32 / ROWS_PER_PASS];  // QKV: RoPE entries of the lane's 4 pairs
+    // QKV store-phase geometry: the lane's 8 columns n .. n+7 hold pairs (n mod 64)/2 .. +3 of a q, k or v section
+    const int seg_n = out_n0 + (lane % LANES_PER_ROW) * 8;
+    const bool seg_rot = EPI == FF_EPI_QKV_ROPE && seg_n < 2 * C3;
+    const float seg_qs = seg_n < C3 ? args.q_scale : 1.f;
+    auto load_row = [&](int j) __attribute__((always_inline)) {
+      const int m = min(m_base + 32 * j + fr, M - 1);  // rows past M are computed on clamped inputs, never stored
+      rs = args.row_scale[m];
+    };
+    auto load_rope = [&](int j) __attribute__((always_inline)) {
+      if constexpr (EPI == FF_EPI_QKV_ROPE) {
+        if (seg_rot) {
+#pragma unroll
+          for (int p = 0; p < 32 / ROWS_PER_PASS; ++p) {
+            const int gm = min(m_base + 32 * j + p * ROWS_PER_PASS + lane / LANES_PER_ROW, M - 1);
+            const int t = (gm % args.rope_len) * 32 + ((seg_n & 63) >> 1);
+            tco[p] = *reinterpret_cast<const float4_t*>(args.rope_cos + t);
+            tsi[p] = *reinterpret_cast<const float4_t*>(args.rope_sin + t);
+          }
+        }
+      }
+    };
+    auto load_residual = [&](int j) __attribute__((always_inline)) {
+      if constexpr (EPI == FF_EPI_RESIDUAL) {
+#pragma unroll
+        for (int p = 0; p < 32 / ROWS_PER_PASS; ++p) {
+          const int gm = m_base + 32 * j + p * ROWS_PER_PASS + lane / LANES_PER_ROW;
+          const int gn = out_n0 + (lane % LANES_PER_ROW) * 8;
+          if (gm < M && gn < out_ld)
+            xres[p] = *reinterpret_cast<const half8_t*>(o16 + static_cast<int64_t>(gm) * out_ld + gn);
+        }
+      }
+    };
+    load_row(0);
+    load_residual(0);
+    load_rope(0);
 #pragma unroll
     for (int j = 0; j < MI; ++j) {
-      const int mrow = m_base + 32 * j + fr;
-      const int m = min(mrow, M - 1);  // rows past M are computed on clamped inputs and never stored
-      const float rs = args.row_scale[m];
-      const float* rcos = nullptr;
-      const float* rsin = nullptr;
-      if constexpr (EPI == FF_EPI_QKV_ROPE) {
-        rcos = args.rope_cos + (m % args.rope_len) * 32;
-        rsin = args.rope_sin + (m % args.rope_len) * 32;
-      }
 #pragma unroll
       for (int i = 0; i < NI; ++i)
 #pragma unroll
@@ -146,26 +183,9 @@ __device__ __forceinline__ void store_epilogue(const int16_t_v (&acc)[NI][MI], i
             h[0] = static_cast<half_t>(silu(y[0]) * y[1]);
             h[1] = static_cast<half_t>(silu(y[2]) * y[3]);
             *reinterpret_cast<half2_t*>(stage + fr * RB + c) = h;  // output column c/2, 2 bytes each
+          } else if constexpr (EPI == FF_EPI_QKV_ROPE) {
+            *reinterpret_cast<float4_t*>(stage + fr * RB + 4 * c) = float4_t{y[0], y[1], y[2], y[3]};
           } else {
-            if constexpr (EPI == FF_EPI_QKV_ROPE) {
-              const int n = n_base + c;
-              const int section = n / C3;
-              if (section < 2) {
-                // the two pairs (n, n+1), (n+2, n+3) use table entries (n mod 64)/2 and the next one
-                const int pi = (n & 63) >> 1;
-                const float2 co = *reinterpret_cast<const float2*>(rcos + pi);
-                const float2 si = *reinterpret_cast<const float2*>(rsin + pi);
-                const float qs = section == 0 ? args.q_scale : 1.f;
-                const float c2[2] = {co.x, co.y}, s2[2] = {si.x, si.y};
-#pragma unroll
-                for (int pr = 0; pr < 2; ++pr) {
-                  const float y0 = y[2 * pr], y1 = y[2 * pr + 1];
-                  const float r0 = y0 * c2[pr] - y1 * s2[pr], r1 = y0 * s2[pr] + y1 * c2[pr];
-                  y[2 * pr] = section == 0 ? r0 * qs : r0;
-                  y[2 * pr + 1] = section == 0 ? r1 * qs : r1;
-                }
-              }
-            }
             if constexpr (EPI == FF_EPI_GELU_F16) {
 #pragma unroll
               for (int t = 0; t < 4; ++t) y[t] = gelu_tanh(y[t]);
@@ -182,26 +202,46 @@ __device__ __forceinline__ void store_epilogue(const int16_t_v (&acc)[NI][MI], i
             *reinterpret_cast<half4_t*>(stage + fr * RB + 2 * c) = h;
           }
         }
-      __builtin_amdgcn_wave_barrier();
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (j + 1 < MI) load_row(j + 1);
 #pragma unroll
       for (int p = 0; p < 32 / ROWS_PER_PASS; ++p) {
         const int r = p * ROWS_PER_PASS + lane / LANES_PER_ROW;
         const int seg = lane % LANES_PER_ROW;
-        half8_t h = *reinterpret_cast<const half8_t*>(stage + r * RB + seg * 16);
+        half8_t h;
+        if constexpr (EPI == FF_EPI_QKV_ROPE) {
+          const float4_t ya = *reinterpret_cast<const float4_t*>(stage + r * RB + seg * 32);
+          const float4_t yb = *reinterpret_cast<const float4_t*>(stage + r * RB + seg * 32 + 16);
+          float v[8] = {ya[0], ya[1], ya[2], ya[3], yb[0], yb[1], yb[2], yb[3]};
+          if (seg_rot) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              const float y0 = v[2 * k], y1 = v[2 * k + 1], co = tco[p][k], si = tsi[p][k];
+              const float r0 = y0 * co - y1 * si, r1 = y0 * si + y1 * co;
+              v[2 * k] = r0 * seg_qs;  // seg_qs is exactly 1 for k
+              v[2 * k + 1] = r1 * seg_qs;
+            }
+          }
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            asm("" : "+v"(v[t]));  // two roundings (fp32, then fp16), never one fused v_fma_mix
+            h[t] = static_cast<half_t>(v[t]);
+          }
+        } else {
+          h = *reinterpret_cast<const half8_t*>(stage + r * RB + seg * 16);
+        }
         const int gm = m_base + 32 * j + r, gn = out_n0 + seg * 8;
         if (gm < M && gn < out_ld) {
-          half8_t* dst = reinterpret_cast<half8_t*>(o16 + static_cast<int64_t>(gm) * out_ld + gn);
           if constexpr (EPI == FF_EPI_RESIDUAL) {
-            const half8_t x = *dst;
 #pragma unroll
-            for (int t = 0; t < 8; ++t) h[t] = h[t] + x[t];
+            for (int t = 0; t < 8; ++t) h[t] = h[t] + xres[p][t];
           }
-          *dst = h;
+          *reinterpret_cast<half8_t*>(o16 + static_cast<int64_t>(gm) * out_ld + gn) = h;
         }
       }
-      __builtin_amdgcn_wave_barrier();
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (j + 1 < MI) {
+        load_residual(j + 1);
+        load_rope(j + 1);
+      }
     }
   }
 }
@@ -332,6 +372,7 @@ __global__ __launch_bounds__(256, 1) void gemm_s8_pipe_kernel(const GemmArgs arg
   for (; kt + P_STAGES - 1 < KT; ++kt) step(kt, std::true_type{});
   for (; kt < KT; ++kt) step(kt, std::false_type{});
   __syncthreads();  // every wave is done with the ring; reuse it as the epilogue staging area
+  static_assert(4 * stage_bytes<FF_EPI_QKV_ROPE, NI>() <= P_STAGES * P_STAGE, "staging must fit in the ring");
   store_epilogue<EPI, NI, MI>(acc, m0 + wm * WM, n0 + wn * WN, lane, args,
                               smem + wave * stage_bytes<EPI, NI>());
 }
@@ -700,7 +741,8 @@ __global__ __launch_bounds__(256) void gemm_s8_kernel(const GemmArgs args) {
   constexpr int A_LD = BM * (BK / 16) / 256;  // 16-byte chunks per thread per slice
   constexpr int W_LD = BN * (BK / 16) / 256;
   constexpr int STAGE = (BM + BN) * BK;
-  __shared__ __attribute__((aligned(16))) int8_t smem[2 * STAGE];
+  constexpr int SMEM = 2 * STAGE > 4 * stage_bytes<FF_EPI_QKV_ROPE, NI>() ? 2 * STAGE : 4 * stage_bytes<FF_EPI_QKV_ROPE, NI>();
+  __shared__ __attribute__((aligned(16))) int8_t smem[SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -780,7 +822,6 @@ __global__ __launch_bounds__(256) void gemm_s8_kernel(const GemmArgs args) {
     if (kt + 1 < KT) swrite(cur ^ 1);
     __syncthreads();
   }
-  static_assert(4 * stage_bytes<FF_EPI_QKV_ROPE, NI>() <= 2 * STAGE, "staging must fit in the tile buffers");
   store_epilogue<EPI, NI, MI>(acc, m0 + wm * WM, n0 + wn * WN, lane, args,
                               reinterpret_cast<uint8_t*>(smem) + wave * stage_bytes<EPI, NI>());
 }
@@ -846,7 +887,7 @@ extern "C" int ff_gemm_s8(const int8_t* A, const int8_t* W, int64_t M, int64_t N
   if (epi == FF_EPI_QKV_ROPE) {
     if (N % 3 != 0 || (N / 3) % 64 != 0) return fail(FF_EINVAL, "gemm_s8: QKV epilogue needs N = 3C with C % 64 == 0");
     if (!rope_cos || !rope_sin || rope_len <= 0) return fail(FF_EINVAL, "gemm_s8: QKV epilogue needs RoPE tables");
-    if (!aligned(rope_cos, 8) || !aligned(rope_sin, 8)) return fail(FF_EINVAL, "gemm_s8: misaligned RoPE tables");
+    if (!aligned(rope_cos, 16) || !aligned(rope_sin, 16)) return fail(FF_EINVAL, "gemm_s8: misaligned RoPE tables");
   }
   if (M == 0) return FF_OK;
   if (!A || !W || !out) return fail(FF_EINVAL, "gemm_s8: null pointer");
