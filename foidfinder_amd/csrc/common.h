@@ -25,6 +25,9 @@ void set_error(const std::string& msg);
 void clear_error();
 int fail(int code, const std::string& msg);
 int check_launch(const char* what);
+// Workgroups of `kernel` (launched with `block` threads and `smem` dynamic LDS bytes) that the current device holds
+// resident at once, over all CUs; cached per kernel, device and shape. 0 if the runtime cannot tell.
+int64_t resident_blocks(const void* kernel, int block, size_t smem);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 

@@ -14,9 +14,12 @@
 //    (IEEE rounding is sign-symmetric and fma(p, +-1, u) rounds once, like the reference's add and subtract).
 //
 // The butterfly stage order, the LayerNorm reduction order and every rounding match oracle/rotq8.py bit for bit (this
-// file is compiled with -ffp-contract=off and correctly rounded fp32 division and sqrt).
+// file is compiled with -ffp-contract=off and correctly rounded fp32 division and sqrt; the LayerNorm's variance
+// accumulation and affine step are explicit fused multiply-adds, as the reference's compiler contracts them).
 //
 // Reference: foidfinder/backends/cuda/csrc/kernels.cu:13-160 (rot_q8_1024_kernel, rot_q8_h128_kernel).
+#include <algorithm>
+
 #include "common.h"
 
 namespace ff {
@@ -34,10 +37,27 @@ __device__ __forceinline__ float swz_xor16(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
 }
 
-// Sign-tracked butterfly across lanes: partner p, own u, s = +1 (column bit 0) or -1 (column bit 1).
-template <int CTRL>
-__device__ __forceinline__ float bfly(float u, float s) {
-  return __builtin_fmaf(dpp<CTRL>(u), s, u);
+// Sign-tracked butterfly across lanes, u = fma(p, s, u) with partner p, own u, s = +1 (column bit 0) or -1 (column
+// bit 1), as one v_fmac_f32_dpp (DPP on the multiplicand: the partner's u). The compiler only emits it as
+// v_mov_b32_dpp + v_fmac_f32, so it is written out; one stage is one call over all of a lane's values, which are
+// distinct registers, so the only VALU-write -> DPP-read hazard (2 wait states) is with whatever wrote them before
+// the stage: the leading s_nop covers it. DPP controls: l^1 quad_perm [1,0,3,2], l^3 quad_perm [3,2,1,0], l^7
+// row_half_mirror, l^15 row_mirror (all partners are inside the 16-lane DPP row, so bound_ctrl never applies).
+#define FF_FMAC_DPP(CTL) "v_fmac_f32_dpp %0, %0, %1 " CTL " row_mask:0xf bank_mask:0xf bound_ctrl:1"
+template <int CTRL, int N>
+__device__ __forceinline__ void bfly_stage(float (&v)[N], float s) {
+  asm volatile("s_nop 1" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    if constexpr (CTRL == DPP_XOR1)
+      asm volatile(FF_FMAC_DPP("quad_perm:[1,0,3,2]") : "+v"(v[i]) : "v"(s));
+    else if constexpr (CTRL == DPP_XOR3)
+      asm volatile(FF_FMAC_DPP("quad_perm:[3,2,1,0]") : "+v"(v[i]) : "v"(s));
+    else if constexpr (CTRL == DPP_XOR7)
+      asm volatile(FF_FMAC_DPP("row_half_mirror") : "+v"(v[i]) : "v"(s));
+    else
+      asm volatile(FF_FMAC_DPP("row_mirror") : "+v"(v[i]) : "v"(s));
+  }
 }
 
 __device__ __forceinline__ float gray_sign(int bit) { return bit ? -1.f : 1.f; }
@@ -89,241 +109,294 @@ __device__ __forceinline__ float half_wave_max(float v) {
 // One row of 1024 per 32-lane half-wave. Reference lane L = 16 c7 + gray(l & 15) of the half owns columns
 // j*256 + L*8 + e (j 0..3, e 0..7), the reference's column layout (kernels.cu:11-12), held by physical lane
 // l = 16 c7 + gray^-1(L & 15). Stage order: column bits 0, 1, 2 (registers e), 8, 9 (registers j), 3..7 (lanes; the
-// last one, bit 7 = lane bit 4, through ds_swizzle). 8 rows per 256-thread workgroup.
+// last one, bit 7 = lane bit 4, through ds_swizzle). 256-thread workgroups of 8 half-waves stride over the rows, each
+// half-wave loading its next row while it transforms the current one; LayerNorm's gamma and beta sit in LDS, loaded
+// once per workgroup.
 template <bool NORM>
 __global__ __launch_bounds__(256) void rot_q8_1024_kernel(const half_t* __restrict__ x, const float* __restrict__ gamma,
                                                           const float* __restrict__ beta, float eps, int64_t T,
                                                           int8_t* __restrict__ out, float* __restrict__ row_scale) {
+  __shared__ float4_t gb[NORM ? 512 : 1];  // gamma as 256 float4, then beta
+  if constexpr (NORM) {
+    for (int i = threadIdx.x; i < 512; i += 256)
+      gb[i] = i < 256 ? reinterpret_cast<const float4_t*>(gamma)[i] : reinterpret_cast<const float4_t*>(beta)[i - 256];
+    __syncthreads();
+  }
   const int lane = threadIdx.x & 31;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 5);
-  if (row >= T) return;  // whole half-waves exit together; cross-lane operations below stay inside the half
   const int l16 = lane & 15, gl = l16 ^ (l16 >> 1);
   const int L = (lane & 16) | gl;  // reference lane = column bits 3..7
-  const half_t* xr = x + row * 1024;
-  float v[32];
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 8;
+  int64_t row = static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 5);
+  // whole half-waves share a row; cross-lane operations below stay inside the half
+  half8_t nxt[4];
+  auto load = [&](int64_t r) __attribute__((always_inline)) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const half8_t h = *reinterpret_cast<const half8_t*>(xr + j * 256 + L * 8);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[j * 8 + e] = static_cast<float>(h[e]);
-  }
-  if constexpr (NORM) {
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) s = s + v[i];
-    const float mean = ref_tree_sum(s) * (1.f / 1024.f);
-    float sq = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      v[i] = v[i] - mean;
-      sq = sq + v[i] * v[i];
-    }
-    const float var = ref_tree_sum(sq) * (1.f / 1024.f);
-    const float rstd = 1.f / sqrtf(var + eps);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = j * 256 + L * 8;
-      const float4_t g0 = *reinterpret_cast<const float4_t*>(gamma + c);
-      const float4_t g1 = *reinterpret_cast<const float4_t*>(gamma + c + 4);
-      const float4_t b0 = *reinterpret_cast<const float4_t*>(beta + c);
-      const float4_t b1 = *reinterpret_cast<const float4_t*>(beta + c + 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[j * 8 + e] = v[j * 8 + e] * rstd * g0[e] + b0[e];
-        v[j * 8 + 4 + e] = v[j * 8 + 4 + e] * rstd * g1[e] + b1[e];
-      }
-    }
-  }
-  // column bits 0, 1, 2 (registers e)
-#pragma unroll
-  for (int h = 1; h < 8; h <<= 1)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (!(e & h)) {
-          const float a = v[j * 8 + e], b = v[j * 8 + e + h];
-          v[j * 8 + e] = a + b;
-          v[j * 8 + e + h] = a - b;
-        }
-  // column bits 8, 9 (registers j)
-#pragma unroll
-  for (int h = 1; h < 4; h <<= 1)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (!(j & h))
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float a = v[j * 8 + e], b = v[(j + h) * 8 + e];
-          v[j * 8 + e] = a + b;
-          v[(j + h) * 8 + e] = a - b;
-        }
-  // column bits 3..7 (lanes)
+    for (int j = 0; j < 4; ++j) nxt[j] = *reinterpret_cast<const half8_t*>(x + r * 1024 + j * 256 + L * 8);
+  };
+  if (row < T) load(row);
   const float s3 = gray_sign(L & 1), s4 = gray_sign(L & 2), s5 = gray_sign(L & 4), s6 = gray_sign(L & 8);
   const float s7 = gray_sign(L & 16);
+  for (; row < T; row += stride) {
+    float v[32];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) v[i] = bfly<DPP_XOR1>(v[i], s3);
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-  for (int i = 0; i < 32; ++i) v[i] = bfly<DPP_XOR3>(v[i], s4);
+      for (int e = 0; e < 8; ++e) v[j * 8 + e] = static_cast<float>(nxt[j][e]);
+    if (row + stride < T) load(row + stride);
+    if constexpr (NORM) {
+      float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) v[i] = bfly<DPP_XOR7>(v[i], s5);
+      for (int i = 0; i < 32; ++i) s = s + v[i];
+      const float mean = ref_tree_sum(s) * (1.f / 1024.f);
+      float sq = 0.f;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) v[i] = bfly<DPP_XOR15>(v[i], s6);
+      for (int i = 0; i < 32; ++i) {
+        v[i] = v[i] - mean;
+        sq = __builtin_fmaf(v[i], v[i], sq);
+      }
+      const float var = ref_tree_sum(sq) * (1.f / 1024.f);
+      const float rstd = 1.f / sqrtf(var + eps);
 #pragma unroll
-  for (int i = 0; i < 32; ++i) v[i] = __builtin_fmaf(swz_xor16(v[i]), s7, v[i]);
-  // v now holds (-1)^popcount(L) times the unnormalized rotation; x 1/32 is exact, so it joins the multiplier
-  float amax = 0.f;
+      for (int j = 0; j < 4; ++j) {
+        const int c4 = (j * 256 + L * 8) >> 2;  // float4 index of the lane's 8 columns
+        const float4_t g0 = gb[c4], g1 = gb[c4 + 1], b0 = gb[256 + c4], b1 = gb[256 + c4 + 1];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  amax = half_wave_max(amax) * 0.03125f;
-  const float scale = fmaxf(amax, 1e-12f) / 127.f;
-  const float inv = 1.f / scale;
-  const float mul = (__builtin_popcount(L) & 1 ? -inv : inv) * 0.03125f;
-  int8_t* orow = out + row * 1024;
+        for (int e = 0; e < 4; ++e) {
+          v[j * 8 + e] = __builtin_fmaf(v[j * 8 + e] * rstd, g0[e], b0[e]);
+          v[j * 8 + 4 + e] = __builtin_fmaf(v[j * 8 + 4 + e] * rstd, g1[e], b1[e]);
+        }
+      }
+    }
+    // column bits 0, 1, 2 (registers e)
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint2 pk;
-    pk.x = pack4(v[j * 8] * mul, v[j * 8 + 1] * mul, v[j * 8 + 2] * mul, v[j * 8 + 3] * mul);
-    pk.y = pack4(v[j * 8 + 4] * mul, v[j * 8 + 5] * mul, v[j * 8 + 6] * mul, v[j * 8 + 7] * mul);
-    *reinterpret_cast<uint2*>(orow + j * 256 + L * 8) = pk;
+    for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (!(e & h)) {
+            const float a = v[j * 8 + e], b = v[j * 8 + e + h];
+            v[j * 8 + e] = a + b;
+            v[j * 8 + e + h] = a - b;
+          }
+    // column bits 8, 9 (registers j)
+#pragma unroll
+    for (int h = 1; h < 4; h <<= 1)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (!(j & h))
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float a = v[j * 8 + e], b = v[(j + h) * 8 + e];
+            v[j * 8 + e] = a + b;
+            v[(j + h) * 8 + e] = a - b;
+          }
+    // column bits 3..7 (lanes)
+    bfly_stage<DPP_XOR1>(v, s3);
+    bfly_stage<DPP_XOR3>(v, s4);
+    bfly_stage<DPP_XOR7>(v, s5);
+    bfly_stage<DPP_XOR15>(v, s6);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = __builtin_fmaf(swz_xor16(v[i]), s7, v[i]);
+    // v now holds (-1)^popcount(L) times the unnormalized rotation; x 1/32 is exact, so it joins the multiplier
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    amax = half_wave_max(amax) * 0.03125f;
+    const float scale = fmaxf(amax, 1e-12f) / 127.f;
+    const float inv = 1.f / scale;
+    const float mul = (__builtin_popcount(L) & 1 ? -inv : inv) * 0.03125f;
+    int8_t* orow = out + row * 1024;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint2 pk;
+      pk.x = pack4(v[j * 8] * mul, v[j * 8 + 1] * mul, v[j * 8 + 2] * mul, v[j * 8 + 3] * mul);
+      pk.y = pack4(v[j * 8 + 4] * mul, v[j * 8 + 5] * mul, v[j * 8 + 6] * mul, v[j * 8 + 7] * mul);
+      *reinterpret_cast<uint2*>(orow + j * 256 + L * 8) = pk;
+    }
+    if (lane == 0) row_scale[row] = scale;
   }
-  if (lane == 0) row_scale[row] = scale;
 }
 
 // One row of C = 128*nb columns per 64-lane wave. Lane 16g + l owns, for i = 0..NI-1, the 8 columns
 // (4i + g)*128 + 8*gray(l) + e of block 4i + g: column bits 0-2 in registers, bits 3-6 across the 16 lanes of a DPP
-// row. Stages run over column bits 0..6 in ascending order, as in kernels.cu:125-135. 4 rows per workgroup.
-// LayerNorm (new; EVA02's norm after SwiGLU): gamma/beta are [C] with zeros past c_real; sums over the real columns
-// run per lane sequentially in (i, e) order, then over lanes by the xor tree 32, 16, 15, 7, 3, 1.
+// row. Stages run over column bits 0..6 in ascending order, as in kernels.cu:125-135. 256-thread workgroups of 4
+// waves stride over the rows, each wave loading its next row while it transforms the current one.
+// LayerNorm (new; EVA02's norm after SwiGLU): gamma/beta are [C] with zeros past c_real, held in LDS (dynamic, 2C
+// floats) for the workgroup's rows; sums over the real columns run per lane sequentially in (i, e) order, then over
+// lanes by the xor tree 32, 16, 15, 7, 3, 1.
 template <int NI, bool NORM>
 __global__ __launch_bounds__(256) void rot_q8_h128_kernel(const half_t* __restrict__ x, int64_t T, int C, int c_real,
                                                           const float* __restrict__ gamma,
                                                           const float* __restrict__ beta, float eps,
                                                           int8_t* __restrict__ out, float* __restrict__ row_scale) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= T) return;  // whole waves exit together
-  const int g = lane >> 4, l16 = lane & 15, gl = l16 ^ (l16 >> 1);
+  extern __shared__ float4_t gbh[];  // NORM: gamma as C/4 float4, then beta
   const int nb = C >> 7;
-  const half_t* xr = x + row * C;
-  float v[NI * 8];
-#pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const int b = 4 * i + g;
-    if (b < nb) {
-      const half8_t h = *reinterpret_cast<const half8_t*>(xr + b * 128 + 8 * gl);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[i * 8 + e] = static_cast<float>(h[e]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[i * 8 + e] = 0.f;
-    }
-  }
   if constexpr (NORM) {
-    int nreal[NI];  // real columns among the lane's 8 of block 4i + g (a prefix)
+    const int n4 = C >> 2;
+    for (int i = threadIdx.x; i < 2 * n4; i += 256)
+      gbh[i] = i < n4 ? reinterpret_cast<const float4_t*>(gamma)[i] : reinterpret_cast<const float4_t*>(beta)[i - n4];
+    __syncthreads();
+  }
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, l16 = lane & 15, gl = l16 ^ (l16 >> 1);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 4;
+  int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);  // whole waves share a row
+  half8_t nxt[NI];
+  auto load = [&](int64_t r) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int b = 4 * i + g;
-      const int left = c_real - (b * 128 + 8 * gl);
-      nreal[i] = b < nb ? (left < 0 ? 0 : (left > 8 ? 8 : left)) : 0;
+      if (b < nb) nxt[i] = *reinterpret_cast<const half8_t*>(x + r * C + b * 128 + 8 * gl);
     }
-    float sum = 0.f;
-#pragma unroll
-    for (int i = 0; i < NI; ++i)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sum = sum + (e < nreal[i] ? v[i * 8 + e] : 0.f);
-    auto tree = [](float t) {
-      t = t + xor_shuffle(t, 32);
-      t = t + swz_xor16(t);
-      t = t + dpp<DPP_XOR15>(t);
-      t = t + dpp<DPP_XOR7>(t);
-      t = t + dpp<DPP_XOR3>(t);
-      return t + dpp<DPP_XOR1>(t);
-    };
-    const float fr = static_cast<float>(c_real);
-    const float mean = tree(sum) / fr;
-    float sq = 0.f;
-#pragma unroll
-    for (int i = 0; i < NI; ++i)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float d = e < nreal[i] ? v[i * 8 + e] - mean : 0.f;
-        v[i * 8 + e] = d;
-        sq = sq + d * d;
-      }
-    const float var = tree(sq) / fr;
-    const float rstd = 1.f / sqrtf(var + eps);
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int b = 4 * i + g;
-      if (b >= nb) continue;  // lanes past the row end keep zeros (they take part in the row's absmax)
-      const int col0 = b * 128 + 8 * gl;  // gamma/beta are zero past c_real: no masking needed inside the row
-      const float4_t g0 = *reinterpret_cast<const float4_t*>(gamma + col0);
-      const float4_t g1 = *reinterpret_cast<const float4_t*>(gamma + col0 + 4);
-      const float4_t b0 = *reinterpret_cast<const float4_t*>(beta + col0);
-      const float4_t b1 = *reinterpret_cast<const float4_t*>(beta + col0 + 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[i * 8 + e] = v[i * 8 + e] * rstd * g0[e] + b0[e];
-        v[i * 8 + 4 + e] = v[i * 8 + 4 + e] * rstd * g1[e] + b1[e];
-      }
-    }
-  }
-  // column bits 0, 1, 2 (registers)
-#pragma unroll
-  for (int h = 1; h < 8; h <<= 1)
-#pragma unroll
-    for (int i = 0; i < NI; ++i)
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (!(e & h)) {
-          const float a = v[i * 8 + e], b = v[i * 8 + e + h];
-          v[i * 8 + e] = a + b;
-          v[i * 8 + e + h] = a - b;
-        }
-  // column bits 3..6 (lanes, Gray order)
-  const float s3 = gray_sign(gl & 1), s4 = gray_sign(gl & 2), s5 = gray_sign(gl & 4), s6 = gray_sign(gl & 8);
-#pragma unroll
-  for (int i = 0; i < NI * 8; ++i) v[i] = bfly<DPP_XOR1>(v[i], s3);
-#pragma unroll
-  for (int i = 0; i < NI * 8; ++i) v[i] = bfly<DPP_XOR3>(v[i], s4);
-#pragma unroll
-  for (int i = 0; i < NI * 8; ++i) v[i] = bfly<DPP_XOR7>(v[i], s5);
-#pragma unroll
-  for (int i = 0; i < NI * 8; ++i) v[i] = bfly<DPP_XOR15>(v[i], s6);
-  // x fp32(1/sqrt(128)) is a rounded multiply (kernels.cu:138); rounding is sign-symmetric, so it may act on the
-  // sign-tracked values
-  float amax = 0.f;
-#pragma unroll
-  for (int i = 0; i < NI * 8; ++i) {
-    v[i] = v[i] * 0.08838834764831845f;
-    amax = fmaxf(amax, fabsf(v[i]));
-  }
-  amax = wave_max(amax);
-  const float scale = fmaxf(amax, 1e-12f) / 127.f;
-  const float inv = 1.f / scale;
-  const float mul = __builtin_popcount(gl) & 1 ? -inv : inv;
-  int8_t* orow = out + row * C;
+  };
+  if (row < T) load(row);
+  int nreal[NI];  // real columns among the lane's 8 of block 4i + g (a prefix)
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int b = 4 * i + g;
-    if (b < nb) {
-      uint2 pk;
-      pk.x = pack4(v[i * 8] * mul, v[i * 8 + 1] * mul, v[i * 8 + 2] * mul, v[i * 8 + 3] * mul);
-      pk.y = pack4(v[i * 8 + 4] * mul, v[i * 8 + 5] * mul, v[i * 8 + 6] * mul, v[i * 8 + 7] * mul);
-      *reinterpret_cast<uint2*>(orow + b * 128 + 8 * gl) = pk;
-    }
+    const int left = c_real - (b * 128 + 8 * gl);
+    nreal[i] = b < nb ? (left < 0 ? 0 : (left > 8 ? 8 : left)) : 0;
   }
-  if (lane == 0) row_scale[row] = scale;
+  const float s3 = gray_sign(gl & 1), s4 = gray_sign(gl & 2), s5 = gray_sign(gl & 4), s6 = gray_sign(gl & 8);
+  for (; row < T; row += stride) {
+    float v[NI * 8];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int b = 4 * i + g;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[i * 8 + e] = b < nb ? static_cast<float>(nxt[i][e]) : 0.f;
+    }
+    if (row + stride < T) load(row + stride);
+    if constexpr (NORM) {
+      // Only block groups past column c_real - 512 can hold padding or the row end (uniform test): the others skip
+      // the masks. The per-lane counts are re-read opaquely each row so that the compiler cannot hoist 8 * NI
+      // loop-invariant lane masks into scalar registers (they would spill).
+      int nr[NI];
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        nr[i] = nreal[i];
+        asm volatile("" : "+v"(nr[i]));
+      }
+      float sum = 0.f;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        if ((4 * i + 4) * 128 > c_real) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sum = sum + (e < nr[i] ? v[i * 8 + e] : 0.f);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sum = sum + v[i * 8 + e];
+        }
+      }
+      auto tree = [](float t) {
+        t = t + xor_shuffle(t, 32);
+        t = t + swz_xor16(t);
+        t = t + dpp<DPP_XOR15>(t);
+        t = t + dpp<DPP_XOR7>(t);
+        t = t + dpp<DPP_XOR3>(t);
+        return t + dpp<DPP_XOR1>(t);
+      };
+      const float fr = static_cast<float>(c_real);
+      const float mean = tree(sum) / fr;
+      float sq = 0.f;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        if ((4 * i + 4) * 128 > c_real) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float d = e < nr[i] ? v[i * 8 + e] - mean : 0.f;
+            v[i * 8 + e] = d;
+            sq = __builtin_fmaf(d, d, sq);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float d = v[i * 8 + e] - mean;
+            v[i * 8 + e] = d;
+            sq = __builtin_fmaf(d, d, sq);
+          }
+        }
+      }
+      const float var = tree(sq) / fr;
+      const float rstd = 1.f / sqrtf(var + eps);
+      const int n4 = C >> 2;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int b = 4 * i + g;
+        if (b >= nb) continue;  // lanes past the row end keep zeros (they take part in the row's absmax)
+        const int c4 = (b * 128 + 8 * gl) >> 2;  // gamma/beta are zero past c_real: no masking inside the row
+        const float4_t g0 = gbh[c4], g1 = gbh[c4 + 1], b0 = gbh[n4 + c4], b1 = gbh[n4 + c4 + 1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[i * 8 + e] = __builtin_fmaf(v[i * 8 + e] * rstd, g0[e], b0[e]);
+          v[i * 8 + 4 + e] = __builtin_fmaf(v[i * 8 + 4 + e] * rstd, g1[e], b1[e]);
+        }
+      }
+    }
+    // column bits 0, 1, 2 (registers)
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (!(e & h)) {
+            const float a = v[i * 8 + e], b = v[i * 8 + e + h];
+            v[i * 8 + e] = a + b;
+            v[i * 8 + e + h] = a - b;
+          }
+    // column bits 3..6 (lanes, Gray order)
+    bfly_stage<DPP_XOR1>(v, s3);
+    bfly_stage<DPP_XOR3>(v, s4);
+    bfly_stage<DPP_XOR7>(v, s5);
+    bfly_stage<DPP_XOR15>(v, s6);
+    // x fp32(1/sqrt(128)) is a rounded multiply (kernels.cu:138); rounding is sign-symmetric, so it may act on the
+    // sign-tracked values
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < NI * 8; ++i) {
+      v[i] = v[i] * 0.08838834764831845f;
+      amax = fmaxf(amax, fabsf(v[i]));
+    }
+    amax = wave_max(amax);
+    const float scale = fmaxf(amax, 1e-12f) / 127.f;
+    const float inv = 1.f / scale;
+    const float mul = __builtin_popcount(gl) & 1 ? -inv : inv;
+    int8_t* orow = out + row * C;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int b = 4 * i + g;
+      if (b < nb) {
+        uint2 pk;
+        pk.x = pack4(v[i * 8] * mul, v[i * 8 + 1] * mul, v[i * 8 + 2] * mul, v[i * 8 + 3] * mul);
+        pk.y = pack4(v[i * 8 + 4] * mul, v[i * 8 + 5] * mul, v[i * 8 + 6] * mul, v[i * 8 + 7] * mul);
+        *reinterpret_cast<uint2*>(orow + b * 128 + 8 * gl) = pk;
+      }
+    }
+    if (lane == 0) row_scale[row] = scale;
+  }
+}
+
+// Grid of a grid-stride rotation kernel: one workgroup per `rows` rows, capped at what the device holds resident
+// (every workgroup then streams rows with its next row's loads in flight, and no workgroup waits for a slot).
+static dim3 stride_grid(const void* kernel, size_t smem, int64_t T, int rows) {
+  int64_t cap = resident_blocks(kernel, 256, smem);
+  if (cap <= 0) cap = 2048;
+  return dim3(static_cast<unsigned>(std::min<int64_t>((T + rows - 1) / rows, cap)));
 }
 
 template <int NI>
-static void launch_h128(dim3 grid, hipStream_t st, const half_t* x, int64_t T, int C, int c_real, const float* g,
-                        const float* b, float eps, int8_t* out, float* rs) {
-  if (g)
-    rot_q8_h128_kernel<NI, true><<<grid, 256, 0, st>>>(x, T, C, c_real, g, b, eps, out, rs);
-  else
+static void launch_h128(hipStream_t st, const half_t* x, int64_t T, int C, int c_real, const float* g, const float* b,
+                        float eps, int8_t* out, float* rs) {
+  if (g) {
+    const size_t smem = 2 * C * sizeof(float);
+    const dim3 grid = stride_grid(reinterpret_cast<const void*>(&rot_q8_h128_kernel<NI, true>), smem, T, 4);
+    rot_q8_h128_kernel<NI, true><<<grid, 256, smem, st>>>(x, T, C, c_real, g, b, eps, out, rs);
+  } else {
+    const dim3 grid = stride_grid(reinterpret_cast<const void*>(&rot_q8_h128_kernel<NI, false>), 0, T, 4);
     rot_q8_h128_kernel<NI, false><<<grid, 256, 0, st>>>(x, T, C, c_real, g, b, eps, out, rs);
+  }
 }
 
 }  // namespace ff
@@ -342,14 +415,15 @@ extern "C" int ff_rot_q8_1024(const void* x, const float* gamma, const float* be
   if (gamma && !(eps > 0.f)) return fail(FF_EINVAL, "rot_q8_1024: eps must be > 0");
   if (!aligned(x, 16) || !aligned(out, 8) || !aligned(row_scale, 4) || (gamma && (!aligned(gamma, 16) || !aligned(beta, 16))))
     return fail(FF_EINVAL, "rot_q8_1024: misaligned pointer");
-  const int64_t blocks = (T + 7) / 8;
-  if (blocks > 0x7fffffff) return fail(FF_EINVAL, "rot_q8_1024: T too large");
-  const dim3 grid(static_cast<unsigned>(blocks));
+  // grid-stride: each half-wave takes every (8 * grid)-th row
   const half_t* px = static_cast<const half_t*>(x);
-  if (gamma)
+  if (gamma) {
+    const dim3 grid = stride_grid(reinterpret_cast<const void*>(&rot_q8_1024_kernel<true>), 0, T, 8);
     rot_q8_1024_kernel<true><<<grid, 256, 0, as_stream(stream)>>>(px, gamma, beta, eps, T, out, row_scale);
-  else
+  } else {
+    const dim3 grid = stride_grid(reinterpret_cast<const void*>(&rot_q8_1024_kernel<false>), 0, T, 8);
     rot_q8_1024_kernel<false><<<grid, 256, 0, as_stream(stream)>>>(px, nullptr, nullptr, eps, T, out, row_scale);
+  }
   return check_launch("rot_q8_1024");
 }
 
@@ -366,9 +440,6 @@ extern "C" int ff_rot_q8_h128(const void* x, int64_t T, int64_t C, int64_t c_rea
   if (!x || !out || !row_scale) return fail(FF_EINVAL, "rot_q8_h128: null pointer");
   if (!aligned(x, 16) || !aligned(out, 8) || !aligned(row_scale, 4) || (gamma && (!aligned(gamma, 16) || !aligned(beta, 16))))
     return fail(FF_EINVAL, "rot_q8_h128: misaligned pointer");
-  const int64_t blocks = (T + 3) / 4;
-  if (blocks > 0x7fffffff) return fail(FF_EINVAL, "rot_q8_h128: T too large");
-  const dim3 grid(static_cast<unsigned>(blocks));
   const int nb = static_cast<int>(C / 128);
   const int ni = (nb + 3) / 4;
   const int cr = gamma ? static_cast<int>(c_real) : static_cast<int>(C);
@@ -376,18 +447,18 @@ extern "C" int ff_rot_q8_h128(const void* x, int64_t T, int64_t C, int64_t c_rea
   hipStream_t st = as_stream(stream);
   const int Ci = static_cast<int>(C);
   switch (ni) {
-    case 1: launch_h128<1>(grid, st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 2: launch_h128<2>(grid, st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 3: launch_h128<3>(grid, st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 4: launch_h128<4>(grid, st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 5: launch_h128<5>(grid, st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 6: launch_h128<6>(grid, st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 7: launch_h128<7>(grid, st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 8: launch_h128<8>(grid, st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 9: launch_h128<9>(grid, st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 10: launch_h128<10>(grid, st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 11: launch_h128<11>(grid, st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 12: launch_h128<12>(grid, st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
+    case 1: launch_h128<1>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
+    case 2: launch_h128<2>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
+    case 3: launch_h128<3>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
+    case 4: launch_h128<4>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
+    case 5: launch_h128<5>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
+    case 6: launch_h128<6>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
+    case 7: launch_h128<7>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
+    case 8: launch_h128<8>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
+    case 9: launch_h128<9>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
+    case 10: launch_h128<10>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
+    case 11: launch_h128<11>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
+    case 12: launch_h128<12>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
     default: return fail(FF_EINVAL, "rot_q8_h128: unsupported C");
   }
   return check_launch("rot_q8_h128");

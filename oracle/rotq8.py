@@ -11,6 +11,8 @@ from __future__ import annotations
 
 import numpy as np
 
+from .gemm import fma32
+
 F32 = np.float32
 INV_SQRT_128 = F32(0.08838834764831845)  # kernels.cu:138, rounded to fp32 once
 EPS_SCALE = F32(1e-12)  # kernels.cu:97
@@ -57,8 +59,10 @@ def layer_norm_1024(v: np.ndarray, gamma: np.ndarray, beta: np.ndarray, eps: flo
 
     Lane L of the 32-lane group owns columns j*256 + L*8 + e and sums them sequentially in (j, e) order; the 32
     partial sums are then combined by the xor tree 16, 8, 4, 2, 1 (common.cuh:58-62). The variance repeats this on
-    (v - mean)^2. rstd = 1 / sqrt(var + eps) with IEEE sqrt and division (the reference's rsqrtf is an
-    approximate instruction; this restatement fixes the correctly rounded form). No fused multiply-add anywhere."""
+    (v - mean)^2, accumulated as fma(d, d, sq). rstd = 1 / sqrt(var + eps) with IEEE sqrt and division (the
+    reference's rsqrtf is an approximate instruction; this restatement fixes the correctly rounded form). Output
+    fma((v - mean) * rstd, gamma, beta). The two fused multiply-adds are where the reference's compiler contracts
+    `sq += d * d` and `d * rstd * g + b` (kernels.cu:80-91); every other operation rounds on its own."""
     T = v.shape[0]
     lanes = v.reshape(T, 4, 32, 8).transpose(0, 2, 1, 3).reshape(T, 32, 32)  # [row, lane, i = j*8 + e]
     s = np.zeros((T, 32), F32)
@@ -69,10 +73,10 @@ def layer_norm_1024(v: np.ndarray, gamma: np.ndarray, beta: np.ndarray, eps: flo
     dl = d.reshape(T, 4, 32, 8).transpose(0, 2, 1, 3).reshape(T, 32, 32)
     sq = np.zeros((T, 32), F32)
     for i in range(32):
-        sq = sq + dl[:, :, i] * dl[:, :, i]
+        sq = fma32(dl[:, :, i], dl[:, :, i], sq)
     var = _xor_tree(sq, (16, 8, 4, 2, 1)) * F32(1.0 / 1024.0)
     rstd = F32(1.0) / np.sqrt(var + F32(eps))
-    return (d * rstd[:, None]) * gamma.astype(F32)[None, :] + beta.astype(F32)[None, :]
+    return fma32(d * rstd[:, None], gamma.astype(F32)[None, :], beta.astype(F32)[None, :])
 
 
 def rot_q8_1024(
@@ -97,8 +101,9 @@ def layer_norm_h128(v: np.ndarray, c_real: int, gamma: np.ndarray, beta: np.ndar
     lane 16g + l owns, for i = 0, 1, ..., the columns (4i + g)*128 + 8*gray(l) + e (e = 0..7, gray(l) = l ^ (l >> 1))
     and sums the real ones sequentially in (i, e) order; the 64 partial sums are combined by the xor tree over lanes
     32, 16, 15, 7, 3, 1. mean = sum / c_real and var = sumsq / c_real are IEEE divisions; rstd = 1 / sqrt(var + eps).
-    No fused multiply-add. (The reference has no such fused norm: its CUDA path is PixAI's GELU MLP. The op order
-    follows the EVA02 SwiGLU + LayerNorm of foidfinder/backends/mlx/kernels.py:31-72.)"""
+    As in layer_norm_1024, the squares accumulate as fma(d, d, sq) and the output is fma(d * rstd, gamma, beta).
+    (The reference has no such fused norm: its CUDA path is PixAI's GELU MLP. The op order follows the EVA02 SwiGLU +
+    LayerNorm of foidfinder/backends/mlx/kernels.py:31-72.)"""
     T, C = v.shape
     nb = C // 128
     ni = (nb + 3) // 4
@@ -123,14 +128,14 @@ def layer_norm_h128(v: np.ndarray, c_real: int, gamma: np.ndarray, beta: np.ndar
     dg = np.where(valid[None], d[:, safe], F32(0.0))
     sq = np.zeros((T, 64), F32)
     for k in range(ni * 8):
-        sq = sq + dg[:, :, k] * dg[:, :, k]
+        sq = fma32(dg[:, :, k], dg[:, :, k], sq)
     var = _xor_tree(sq, masks) / F32(c_real)
     rstd = F32(1.0) / np.sqrt(var + F32(eps))
     g_full = np.zeros(C, F32)
     b_full = np.zeros(C, F32)
     g_full[:c_real] = gamma
     b_full[:c_real] = beta
-    y = (d * rstd[:, None]) * g_full[None, :] + b_full[None, :]
+    y = fma32(d * rstd[:, None], g_full[None, :], b_full[None, :])
     return np.where(real[None, :], y, F32(0.0)).astype(F32)
 
 
