@@ -21,6 +21,8 @@
 // Reference: foidfinder/backends/cuda/csrc/gemm.cuh:14-171 and kernels.cu:167-217.
 #include <type_traits>
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace ff {
@@ -732,6 +734,198 @@ static int launch_wide(const GemmArgs& a, int epi, hipStream_t st) {
   return check_launch("gemm_s8");
 }
 
+// ---------------- variant 8: persistent 256 x 256, 8 waves, one workgroup per CU ----------------
+//
+// The variant-6 main loop (two 64 KB slots of K 128), with the ring running on across tiles: the grid holds one
+// workgroup per CU, each takes every G-th tile of the grouped order, and slices are one stream, so the next tile's
+// first slice loads under the current tile's last MFMAs and its first fragments are read before the epilogue. No
+// workgroup starts cold, and row tiles that reach past M are ordered last (their rows past M load as zeros, and
+// MFMAs on zeros draw less power, so the partial last round runs at a higher clock). The epilogue stages through
+// the ring slot of the tile's last slice, which no load targets until the barrier after the epilogue; when eight
+// staging areas do not fit in one slot (QKV), the last ones use a spare area past the ring.
+
+template <int EPI>
+__global__ __launch_bounds__(512, 1) void gemm_s8_persist_kernel(const GemmArgs args) {
+  constexpr int RK = 128, BM = 256, BN = 256, WM = 128, WN = 64, MI = WM / 32, NI = WN / 32;
+  constexpr int STAGE = (BM + BN) * RK;      // 64 KB per ring slot, two slots
+  constexpr int LOADS = STAGE / (512 * 16);  // 16-byte loads per thread per slot
+  constexpr int A_BLOCKS = BM * RK / 1024;   // 1 KB blocks of A per slot; W blocks follow
+  constexpr int CPR = RK / 16;               // 16-byte chunks per row
+  constexpr int KSTEPS = RK / 32;            // 32-byte MFMA k-steps per slot (even: a slot starts in buffer 0)
+  constexpr int SB = stage_bytes<EPI, NI>();
+  constexpr int FIT = STAGE / SB < 8 ? STAGE / SB : 8;  // staging areas inside the free slot
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE + (8 - FIT) * SB];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2, wn = wave & 3;
+  const int M = args.M, N = args.N, K = args.K, KT = K / RK;
+  const int tiles_n = (N + BN - 1) / BN, full_m = M / BM, tiles_m = (M + BM - 1) / BM;
+  const int ntiles = tiles_m * tiles_n, G = gridDim.x;
+  const int first = xcd_remap(blockIdx.x, G);  // this workgroup's tiles: first, first + G, ...
+  const int my_tiles = first < ntiles ? (ntiles - 1 - first) / G + 1 : 0;
+  const int total = my_tiles * KT;             // slices this workgroup streams
+  // Tile r of this workgroup: full row tiles in groups of R_GROUP_M row tiles (column-major inside a group), then
+  // the partial row tile.
+  auto coords = [&](int r, int& m0, int& n0) __attribute__((always_inline)) {
+    const int L = first + r * G;
+    if (L < full_m * tiles_n) {
+      const int per_group = R_GROUP_M * tiles_n;
+      const int g = L / per_group, in_g = L % per_group;
+      const int gm = min(R_GROUP_M, full_m - g * R_GROUP_M);
+      m0 = (g * R_GROUP_M + in_g % gm) * BM;
+      n0 = (in_g / gm) * BN;
+    } else {
+      m0 = full_m * BM;
+      n0 = (L - full_m * tiles_n) * BN;
+    }
+  };
+
+  auto nrec = [](int64_t bytes) { return static_cast<int>(bytes < 0x7fffffff ? bytes : 0x7fffffff); };
+  // Load side: slice `ig` (kt `ikt` of tile `ir`, at rows im0 / columns in0) goes to ring slot ig & 1.
+  int ig = 0, ir = 0, ikt = 0, im0 = 0, in0 = 0;
+  if (my_tiles > 0) coords(0, im0, in0);
+  auto issue = [&]() __attribute__((always_inline)) {
+    uint8_t* st = smem + (ig & 1) * STAGE;
+    const int kb = ikt * RK;
+    const int8_t* abase = args.A + static_cast<int64_t>(im0) * K + kb;
+    const int8_t* wbase = args.W + static_cast<int64_t>(in0) * K + kb;
+    const int an = nrec(static_cast<int64_t>(M - im0) * K - kb), wn_ = nrec(static_cast<int64_t>(N - in0) * K - kb);
+    // Lane offsets are recomputed per slice from an opaque copy of the lane index (a few VALU per load) instead of
+    // being held in registers, which would stay live through the epilogue.
+    int l = lane;
+    asm volatile("" : "+v"(l));
+#pragma unroll
+    for (int p = 0; p < LOADS; ++p) {
+      const int blk = wave * LOADS + p;  // wave-uniform
+      const int row = (blk < A_BLOCKS ? blk : blk - A_BLOCKS) * (1024 / RK) + l / CPR, chunk = l % CPR;
+      const uint32_t voff = static_cast<uint32_t>(row * K + ((wswz<RK>(row, chunk) - row * RK)));
+      if (blk < A_BLOCKS)
+        buffer_to_lds(abase, an, st + blk * 1024, voff);
+      else
+        buffer_to_lds(wbase, wn_, st + blk * 1024, voff);
+    }
+    ++ig;
+    if (++ikt == KT) {
+      ikt = 0;
+      if (++ir < my_tiles) coords(ir, im0, in0);
+    }
+  };
+
+  int16_t_v acc[NI][MI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+#pragma unroll
+    for (int j = 0; j < MI; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  const int fr = lane & 31, fk = lane >> 5;
+  int4_t xw[2][NI], ya[2][MI];
+  auto read_frags = [&](int g, int kk, int b) __attribute__((always_inline)) {
+    const uint8_t* sa = smem + (g & 1) * STAGE;
+    const uint8_t* sw = sa + BM * RK;
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      xw[b][i] = *reinterpret_cast<const int4_t*>(sw + wswz<RK>(wn * WN + i * 32 + fr, 2 * kk + fk));
+#pragma unroll
+    for (int j = 0; j < MI; ++j)
+      ya[b][j] = *reinterpret_cast<const int4_t*>(sa + wswz<RK>(wm * WM + j * 32 + fr, 2 * kk + fk));
+  };
+
+  if (total == 0) return;
+  issue();
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  read_frags(0, 0, 0);
+  int kt = 0, r = 0, m0, n0;
+  coords(0, m0, n0);
+  // Slice g: slice g + 1 is issued into the other slot (free: every wave passed the barrier after reading it);
+  // the k-steps run in order, each while the next one's fragments are read; before the last one, slice g + 1 is
+  // waited for (and the barrier passed), so its first fragments are read while slice g's last k-step computes.
+  // After a tile's last slice they are read once more after the epilogue; after the final slice the reads hit a
+  // stale slot and are never used.
+  auto slice = [&](int g) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+      const int b = kk & 1;
+      if (kk + 1 < KSTEPS) {
+        read_frags(g, kk + 1, b ^ 1);
+      } else {
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        read_frags(g + 1, 0, b ^ 1);
+      }
+#pragma unroll
+      for (int j = 0; j < MI; ++j)
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xw[b][i], ya[b][j], acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int x = 0; x < NI + MI; ++x) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, NI * MI - (NI + MI), 0);
+    }
+  };
+  for (int g = 0; g < total; ++g) {
+    if (g + 1 < total) issue();
+    slice(g);
+    if (++kt == KT) {
+      // Every wave has read all of slice g (barrier above): its slot is the staging area until the barrier below,
+      // after which slice g + 2 may load into it.
+      uint8_t* stage = wave < FIT ? smem + (g & 1) * STAGE + wave * SB : smem + 2 * STAGE + (wave - FIT) * SB;
+      // An opaque lane index keeps the epilogue's lane-derived offsets from being hoisted out of the tile loop,
+      // where they would hold registers through the main loop.
+      int el = lane;
+      asm volatile("" : "+v"(el));
+      store_epilogue<EPI, NI, MI>(acc, m0 + wm * WM, n0 + wn * WN, el, args, stage);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      // The next slice's first fragments again: the copies read above are dead on this path, so they do not stay
+      // live through the epilogue.
+      read_frags(g + 1, 0, 0);
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int j = 0; j < MI; ++j)
+#pragma unroll
+          for (int q = 0; q < 16; ++q) acc[i][j][q] = 0;
+      kt = 0;
+      if (++r < my_tiles) coords(r, m0, n0);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+static int launch_persist(const GemmArgs& a, int epi, hipStream_t st) {
+  if (a.K % 128 != 0) return fail(FF_EINVAL, "gemm_s8: K must be a multiple of the slice");
+  const int64_t tiles = static_cast<int64_t>((a.M + 255) / 256) * ((a.N + 255) / 256);
+  if (tiles > 0x7fffffff) return fail(FF_EINVAL, "gemm_s8: too many tiles");
+  const void* kernels[] = {
+      reinterpret_cast<const void*>(&gemm_s8_persist_kernel<FF_EPI_QKV_ROPE>),
+      reinterpret_cast<const void*>(&gemm_s8_persist_kernel<FF_EPI_RESIDUAL>),
+      reinterpret_cast<const void*>(&gemm_s8_persist_kernel<FF_EPI_GELU_F16>),
+      reinterpret_cast<const void*>(&gemm_s8_persist_kernel<FF_EPI_SWIGLU>),
+      reinterpret_cast<const void*>(&gemm_s8_persist_kernel<FF_EPI_BIAS_F16>),
+      reinterpret_cast<const void*>(&gemm_s8_persist_kernel<FF_EPI_I32>),
+  };
+  int64_t resident = resident_blocks(kernels[epi - FF_EPI_QKV_ROPE], 512, 0);
+  if (resident <= 0) resident = 256;
+  const dim3 grid(static_cast<unsigned>(std::min<int64_t>(tiles, resident)));
+  switch (epi) {
+    case FF_EPI_QKV_ROPE: gemm_s8_persist_kernel<FF_EPI_QKV_ROPE><<<grid, 512, 0, st>>>(a); break;
+    case FF_EPI_RESIDUAL: gemm_s8_persist_kernel<FF_EPI_RESIDUAL><<<grid, 512, 0, st>>>(a); break;
+    case FF_EPI_GELU_F16: gemm_s8_persist_kernel<FF_EPI_GELU_F16><<<grid, 512, 0, st>>>(a); break;
+    case FF_EPI_SWIGLU: gemm_s8_persist_kernel<FF_EPI_SWIGLU><<<grid, 512, 0, st>>>(a); break;
+    case FF_EPI_BIAS_F16: gemm_s8_persist_kernel<FF_EPI_BIAS_F16><<<grid, 512, 0, st>>>(a); break;
+    case FF_EPI_I32: gemm_s8_persist_kernel<FF_EPI_I32><<<grid, 512, 0, st>>>(a); break;
+    default: return fail(FF_EINVAL, "gemm_s8: bad epilogue");
+  }
+  return check_launch("gemm_s8");
+}
+
 // ---------------- variants 2, 3: register-staged double buffering ----------------
 
 template <int BM, int BN, int EPI>
@@ -862,8 +1056,8 @@ static int launch_pipe(const GemmArgs& a, int epi, hipStream_t st) {
 // 1: 256 x 256 pipelined (direct-to-LDS, 4 stages); 2: 128 x 128 staged; 3: 256 x 128 staged;
 // 4, 5: 256 x 128 buffer->LDS ring, two workgroups per CU (3 slots of K 64, 6 slots of K 32);
 // 6, 7: 256 x 256, 8 waves, one workgroup per CU (2 slots of K 128 - or variant 7 when K % 128 != 0 -, 4 slots
-// of K 64).
-constexpr int kVariants = 7;
+// of K 64); 8: variant 6 as a persistent grid, the ring streaming across tiles (variant 7 when K % 128 != 0).
+constexpr int kVariants = 8;
 
 }  // namespace ff
 
@@ -920,6 +1114,7 @@ extern "C" int ff_gemm_s8(const int8_t* A, const int8_t* W, int64_t M, int64_t N
     case 5: return launch_ring<32, 6>(a, epi, st);
     case 6: return a.K % 128 == 0 ? launch_wide<128, 2>(a, epi, st) : launch_wide<64, 4>(a, epi, st);
     case 7: return launch_wide<64, 4>(a, epi, st);
+    case 8: return a.K % 128 == 0 ? launch_persist(a, epi, st) : launch_wide<64, 4>(a, epi, st);
   }
   return fail(FF_EINVAL, "gemm_s8: bad variant");
 }

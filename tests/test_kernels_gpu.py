@@ -146,7 +146,7 @@ def run_gemm(dev, a, w, rs, cs, bias, epi, variant, out=None, rope=None, q_scale
     return o.cpu().numpy()
 
 
-GEMM_VARIANTS = [1, 2, 3, 4, 5, 6, 7]  # ff_gemm_s8_variants()
+GEMM_VARIANTS = [1, 2, 3, 4, 5, 6, 7, 8]  # ff_gemm_s8_variants()
 GEMM_SHAPES = [(1, 16, 64), (17, 48, 128), (300, 3072, 1024), (1025, 5632, 1024), (129, 1024, 2816), (257, 272, 192)]
 
 
@@ -185,6 +185,40 @@ def test_gemm_s8_epilogue_bit_exact(dev, rng, epi, variant):
     want = OG.gemm_s8(a, w, rs, cs, bias, epi, **kw)
     if epi == OG.EPI_SWIGLU:
         assert_within_one_fp16_ulp(got, want, f"SwiGLU epilogue, variant {variant}")
+        return
+    bad = np.argwhere(got.view(np.uint16) != want.view(np.uint16))
+    assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[:4].tolist()}: {got[tuple(bad[0])]} vs {want[tuple(bad[0])]}"
+
+
+# More 256 x 256 tiles than an MI355X holds workgroups (256): the persistent variant streams several tiles per
+# workgroup, its K ring running across tile boundaries, and takes the partial row tile last.
+MULTI_TILE_SHAPES = [(4100, 4096, 256), (32800, 1024, 128), (6000, 3072, 384)]
+
+
+@pytest.mark.parametrize(("M", "N", "K"), MULTI_TILE_SHAPES)
+def test_gemm_s8_persistent_multi_tile_int32_bit_exact(dev, rng, M, N, K):
+    a, w, rs, cs, bias = gemm_inputs(rng, M, N, K)
+    got = run_gemm(dev, a, w, rs, cs, bias, OG.EPI_I32, 8)
+    want = OG.gemm_s8_i32(a, w)
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[:4].tolist()}: {got[tuple(bad[0])]} vs {want[tuple(bad[0])]}"
+
+
+@pytest.mark.parametrize("epi", [OG.EPI_BIAS_F16, OG.EPI_RESIDUAL, OG.EPI_QKV_ROPE, OG.EPI_SWIGLU])
+def test_gemm_s8_persistent_multi_tile_epilogues(dev, rng, epi):
+    M, N, K = {OG.EPI_QKV_ROPE: (6000, 3072, 256), OG.EPI_SWIGLU: (4100, 5632, 256)}.get(epi, (32800, 1024, 128))
+    a, w, rs, cs, bias = gemm_inputs(rng, M, N, K)
+    kw, out, rope = {}, None, None
+    if epi == OG.EPI_RESIDUAL:
+        out = rng.standard_normal((M, N)).astype(np.float16)
+        kw["residual"] = out
+    if epi == OG.EPI_QKV_ROPE:
+        rope = OM.eva02_rope_tables(32, 16)
+        kw.update(rope_cos=rope[0], rope_sin=rope[1], q_scale=OM.Q_SCALE)
+    got = run_gemm(dev, a, w, rs, cs, bias, epi, 8, out=out, rope=rope, q_scale=kw.get("q_scale", 1.0))
+    want = OG.gemm_s8(a, w, rs, cs, bias, epi, **kw)
+    if epi == OG.EPI_SWIGLU:
+        assert_within_one_fp16_ulp(got, want, "SwiGLU epilogue, persistent variant")
         return
     bad = np.argwhere(got.view(np.uint16) != want.view(np.uint16))
     assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[:4].tolist()}: {got[tuple(bad[0])]} vs {want[tuple(bad[0])]}"
