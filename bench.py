@@ -204,6 +204,7 @@ def main():
         "roofline": {"kernel": dom, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
                      "unit": dk["unit"], "frac": dk["frac"], "traffic": traffic},
         "kernels": kern,
+        "gemm_variants": {name: eng.variants.get((name, B), 0) for name in ("qkv", "proj", "fc1", "fc2")},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

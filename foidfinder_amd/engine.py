@@ -265,10 +265,14 @@ class Eva02Int8:
         }
 
     def _autotune(self, B: int, buf: dict[str, torch.Tensor]) -> None:
-        """Pick the fastest GEMM tile variant per GEMM for this batch size (engine.py:108-135)."""
-        buf["a8"].zero_()
-        buf["h8"].zero_()
-        buf["rs"].fill_(1.0)
+        """Pick the fastest GEMM tile variant per GEMM for this batch size (engine.py:108-135). The operands are
+        random int8 codes, not zeros: MFMA power and so the clock depend on the data, and zeros would time the
+        variants at a clock that real activations never see."""
+        g = torch.Generator(device=buf["a8"].device).manual_seed(0)
+        for name in ("a8", "h8"):
+            t = buf[name]
+            t.copy_(torch.randint(-127, 128, t.shape, dtype=torch.int8, device=t.device, generator=g))
+        buf["rs"].fill_(1e-2)
         buf["o16"].zero_()
         n = lib().ff_gemm_s8_variants()
         for name, fn in self._gemm_jobs(buf).items():

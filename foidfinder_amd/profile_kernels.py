@@ -24,7 +24,10 @@ def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--reps", type=int, default=3)
+    ap.add_argument("--variants", default="qkv=8,proj=8,fc1=8,fc2=8",
+                    help="GEMM tile variant per GEMM, as the engine's autotune picked them (bench.py prints them)")
     args = ap.parse_args()
+    var = {kv.split("=")[0]: int(kv.split("=")[1]) for kv in args.variants.split(",")}
     k = kernels()
     dev = torch.device("cuda:0")
     cfg = Eva02Config()
@@ -55,14 +58,15 @@ def main() -> None:
         k.rot_q8_1024(x, ones(d), zeros(d), a8, rs, cfg.eps)
         k.rot_q8_1024(o16, None, None, a8, rs, cfg.eps)
         k.rot_q8_h128(h16, h8, rs, *pad_norm(ones(h), zeros(h), hp), h, cfg.eps)
-        k.gemm_s8(a8, w["qkv"], rs, cs["qkv"], zeros(3 * d), out_qkv, EPI_QKV_ROPE, 0, cos, sin, 0.18)
-        k.gemm_s8(a8, w["proj"], rs, cs["proj"], zeros(d), xr, EPI_RESIDUAL, 0, None, None, 1.0)
-        k.gemm_s8(a8, w["fc1"], rs, cs["fc1"], zeros(2 * hp), hout, EPI_SWIGLU, 0, None, None, 1.0)
-        k.gemm_s8(h8, w["fc2"], rs, cs["fc2"], zeros(d), xr, EPI_RESIDUAL, 0, None, None, 1.0)
+        k.gemm_s8(a8, w["qkv"], rs, cs["qkv"], zeros(3 * d), out_qkv, EPI_QKV_ROPE, var["qkv"], cos, sin, 0.18)
+        k.gemm_s8(a8, w["proj"], rs, cs["proj"], zeros(d), xr, EPI_RESIDUAL, var["proj"], None, None, 1.0)
+        k.gemm_s8(a8, w["fc1"], rs, cs["fc1"], zeros(2 * hp), hout, EPI_SWIGLU, var["fc1"], None, None, 1.0)
+        k.gemm_s8(h8, w["fc2"], rs, cs["fc2"], zeros(d), xr, EPI_RESIDUAL, var["fc2"], None, None, 1.0)
         k.attention(qkv, o16, cfg.tokens)
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(f"profile_kernels: {args.reps} reps at batch {args.batch} (M = {M}); copy of {COPY_BYTES} bytes", flush=True)
+    print(f"profile_kernels: {args.reps} reps at batch {args.batch} (M = {M}), GEMM variants {var}; copy of "
+          f"{COPY_BYTES} bytes", flush=True)
 
 
 if __name__ == "__main__":
