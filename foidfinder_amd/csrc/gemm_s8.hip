@@ -43,6 +43,34 @@ struct GemmArgs {
 
 constexpr int BK = 64;
 
+constexpr uint32_t RSRC_WORD3 = 0x00020000;  // buffer descriptor word 3: raw dword access (gfx9 family)
+
+// Raw buffer loads and stores through a descriptor over [base, base + nbytes): an access past the range reads zeros
+// or is dropped, so bounds need no clamped addresses or branches, and the 32-bit lane offset plus a scalar base
+// replaces 64-bit address arithmetic per access. Plain functions, so the descriptor type never appears in a
+// template-dependent expression (the host pass of a template drops its kernel stubs otherwise). An offset of
+// OOB_OFFSET is always out of range (nbytes <= INT32_MAX).
+constexpr uint32_t OOB_OFFSET = 0x80000000u;
+__device__ __forceinline__ int buf_bytes(int64_t bytes) {
+  return static_cast<int>(bytes < 0 ? 0 : (bytes < 0x7fffffff ? bytes : 0x7fffffff));
+}
+__device__ __forceinline__ float4_t buf_load_f4(const void* base, int nbytes, uint32_t voff) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nbytes, RSRC_WORD3);
+  return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+}
+__device__ __forceinline__ float buf_load_f1(const void* base, int nbytes, uint32_t voff) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nbytes, RSRC_WORD3);
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0));
+}
+__device__ __forceinline__ half8_t buf_load_h8(const void* base, int nbytes, uint32_t voff) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nbytes, RSRC_WORD3);
+  return __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+}
+__device__ __forceinline__ void buf_store_h8(half8_t v, void* base, int nbytes, uint32_t voff) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, nbytes, RSRC_WORD3);
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(int4_t, v), r, voff, 0, 0);
+}
+
 // LDS rows of 64 bytes (4 chunks of 16 B); chunk index XOR-swizzled with bits 2-3 of the row. gfx950 serves a
 // 16-byte-per-lane LDS read 16 lanes at a time from 64 four-byte banks (256 B), so the 16 rows read by 16 consecutive
 // lanes must land in 16 distinct 16-byte slots of a 256-byte window: rows r..r+3 fill one window's 4 slots each, and
@@ -115,17 +143,21 @@ __device__ __forceinline__ void store_epilogue(const int16_t_v (&acc)[NI][MI], i
     const int out_ld = SWI ? N / 2 : N;
     const int out_n0 = SWI ? n_base / 2 : n_base;
     const int C3 = N / 3;  // QKV: section width
-    half_t* o16 = static_cast<half_t*>(args.out);
-    // Scale and bias of the wave's 32 NI columns, loaded once per lane column group (i, q) (clamped past N: those
-    // columns are never stored).
+    // The wave's output rows m_base .. m_base + 32 MI - 1 through one descriptor that ends at row M: rows past M
+    // (and the column-masked segments below) are dropped by the range check.
+    half_t* o16 = static_cast<half_t*>(args.out) + static_cast<int64_t>(m_base) * out_ld;
+    const int o_bytes = buf_bytes(static_cast<int64_t>(M - m_base) * out_ld * 2);
+    // Scale and bias of the wave's 32 NI columns, loaded once per lane column group (i, q); past N they read zeros
+    // (those columns are never stored).
     float4_t cs[NI][4], bi[NI][4];
 #pragma unroll
     for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int nc = min(n_base + 32 * i + 8 * q + 4 * fk, N - 4);
-        cs[i][q] = *reinterpret_cast<const float4_t*>(args.col_scale + nc);
-        bi[i][q] = *reinterpret_cast<const float4_t*>(args.bias + nc);
+        const uint32_t off = static_cast<uint32_t>(32 * i + 8 * q + 4 * fk) * 4;
+        const int nb = buf_bytes(static_cast<int64_t>(N - n_base) * 4);
+        cs[i][q] = buf_load_f4(args.col_scale + n_base, nb, off);
+        bi[i][q] = buf_load_f4(args.bias + n_base, nb, off);
       }
     // Per-row inputs are software-pipelined: the row scale of block j + 1 is loaded as soon as block j's results are
     // computed, and the residual rows (or RoPE table rows) of block j + 1 as soon as block j is stored, so their
@@ -136,21 +168,40 @@ __device__ __forceinline__ void store_epilogue(const int16_t_v (&acc)[NI][MI], i
     float4_t tco[32 / ROWS_PER_PASS], tsi[32 / ROWS_PER_PASS];  // QKV: RoPE entries of the lane's 4 pairs
     // QKV store-phase geometry: the lane's 8 columns n .. n+7 hold pairs (n mod 64)/2 .. +3 of a q, k or v section
     const int seg_n = out_n0 + (lane % LANES_PER_ROW) * 8;
-    const bool seg_rot = EPI == FF_EPI_QKV_ROPE && seg_n < 2 * C3;
-    const float seg_qs = seg_n < C3 ? args.q_scale : 1.f;
-    auto load_row = [&](int j) __attribute__((always_inline)) {
-      const int m = min(m_base + 32 * j + fr, M - 1);  // rows past M are computed on clamped inputs, never stored
-      rs = args.row_scale[m];
+    const bool seg_rot = EPI == FF_EPI_QKV_ROPE && seg_n < 2 * C3;  // wave-uniform: sections are 64-aligned
+    const bool seg_q = seg_n < C3;
+    const int row_in_pass = lane / LANES_PER_ROW;
+    // Byte offset of the lane's store segment in row r of the wave (r = 32 j + pass row); OOB_OFFSET masks segments
+    // past the last column (N not a multiple of the wave's columns).
+    const uint32_t seg_off = seg_n < out_ld ? static_cast<uint32_t>(seg_n) * 2 : OOB_OFFSET;
+    auto row_off = [&](int r) __attribute__((always_inline)) {
+      return seg_off == OOB_OFFSET ? OOB_OFFSET : static_cast<uint32_t>(r * out_ld) * 2 + seg_off;
     };
+    auto load_row = [&](int j) __attribute__((always_inline)) {
+      // rows past M read 0 (computed, never stored)
+      rs = buf_load_f1(args.row_scale + m_base, buf_bytes(static_cast<int64_t>(M - m_base) * 4),
+                       static_cast<uint32_t>(32 * j + fr) * 4);
+    };
+    // QKV: RoPE table row (m mod rope_len) of the lane's pass row, kept incrementally: the rows of block j, pass p
+    // are rope_row0 + 32 j + p ROWS_PER_PASS (at most 32 MI - 1 past it), wrapped by at most one subtraction when
+    // rope_len is larger than that span, else by a modulo.
+    int rope_row0 = 0;
+    if constexpr (EPI == FF_EPI_QKV_ROPE) rope_row0 = (m_base + row_in_pass) % args.rope_len;
     auto load_rope = [&](int j) __attribute__((always_inline)) {
       if constexpr (EPI == FF_EPI_QKV_ROPE) {
         if (seg_rot) {
+          const int L = args.rope_len;
+          const int tbytes = L * 32 * 4;  // rope_len <= 2^24 (checked on the host)
 #pragma unroll
           for (int p = 0; p < 32 / ROWS_PER_PASS; ++p) {
-            const int gm = min(m_base + 32 * j + p * ROWS_PER_PASS + lane / LANES_PER_ROW, M - 1);
-            const int t = (gm % args.rope_len) * 32 + ((seg_n & 63) >> 1);
-            tco[p] = *reinterpret_cast<const float4_t*>(args.rope_cos + t);
-            tsi[p] = *reinterpret_cast<const float4_t*>(args.rope_sin + t);
+            int r = rope_row0 + 32 * j + p * ROWS_PER_PASS;
+            if (L >= 32 * MI)
+              r = r >= L ? r - L : r;
+            else
+              r %= L;
+            const uint32_t t = static_cast<uint32_t>(r * 32 + ((seg_n & 63) >> 1)) * 4;
+            tco[p] = buf_load_f4(args.rope_cos, tbytes, t);
+            tsi[p] = buf_load_f4(args.rope_sin, tbytes, t);
           }
         }
       }
@@ -158,12 +209,8 @@ __device__ __forceinline__ void store_epilogue(const int16_t_v (&acc)[NI][MI], i
     auto load_residual = [&](int j) __attribute__((always_inline)) {
       if constexpr (EPI == FF_EPI_RESIDUAL) {
 #pragma unroll
-        for (int p = 0; p < 32 / ROWS_PER_PASS; ++p) {
-          const int gm = m_base + 32 * j + p * ROWS_PER_PASS + lane / LANES_PER_ROW;
-          const int gn = out_n0 + (lane % LANES_PER_ROW) * 8;
-          if (gm < M && gn < out_ld)
-            xres[p] = *reinterpret_cast<const half8_t*>(o16 + static_cast<int64_t>(gm) * out_ld + gn);
-        }
+        for (int p = 0; p < 32 / ROWS_PER_PASS; ++p)
+          xres[p] = buf_load_h8(o16, o_bytes, row_off(32 * j + p * ROWS_PER_PASS + row_in_pass));
       }
     };
     load_row(0);
@@ -218,9 +265,12 @@ __device__ __forceinline__ void store_epilogue(const int16_t_v (&acc)[NI][MI], i
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
               const float y0 = v[2 * k], y1 = v[2 * k + 1], co = tco[p][k], si = tsi[p][k];
-              const float r0 = y0 * co - y1 * si, r1 = y0 * si + y1 * co;
-              v[2 * k] = r0 * seg_qs;  // seg_qs is exactly 1 for k
-              v[2 * k + 1] = r1 * seg_qs;
+              v[2 * k] = y0 * co - y1 * si;
+              v[2 * k + 1] = y0 * si + y1 * co;
+            }
+            if (seg_q) {  // q is scaled after the rotation; k is not (wave-uniform)
+#pragma unroll
+              for (int t = 0; t < 8; ++t) v[t] = v[t] * args.q_scale;
             }
           }
 #pragma unroll
@@ -231,14 +281,11 @@ __device__ __forceinline__ void store_epilogue(const int16_t_v (&acc)[NI][MI], i
         } else {
           h = *reinterpret_cast<const half8_t*>(stage + r * RB + seg * 16);
         }
-        const int gm = m_base + 32 * j + r, gn = out_n0 + seg * 8;
-        if (gm < M && gn < out_ld) {
-          if constexpr (EPI == FF_EPI_RESIDUAL) {
+        if constexpr (EPI == FF_EPI_RESIDUAL) {
 #pragma unroll
-            for (int t = 0; t < 8; ++t) h[t] = h[t] + xres[p][t];
-          }
-          *reinterpret_cast<half8_t*>(o16 + static_cast<int64_t>(gm) * out_ld + gn) = h;
+          for (int t = 0; t < 8; ++t) h[t] = h[t] + xres[p][t];
         }
+        buf_store_h8(h, o16, o_bytes, row_off(32 * j + r));
       }
       if (j + 1 < MI) {
         load_residual(j + 1);
@@ -390,7 +437,6 @@ __global__ __launch_bounds__(256, 1) void gemm_s8_pipe_kernel(const GemmArgs arg
 
 constexpr int R_BM = 256, R_BN = 128;
 constexpr int R_GROUP_M = 8;                 // m-tiles per tile group
-constexpr uint32_t RSRC_WORD3 = 0x00020000;  // buffer descriptor word 3: raw dword access (gfx9 family)
 
 // LDS row layout of a K slice of RK bytes (64: 4 chunks of 16 B, 32: 2 chunks). A 16-byte-per-lane read pass covers
 // 16 rows and 64 banks: with 64-byte rows the chunk XOR bits 2-3 of the row spreads rows r, r+4, r+8, r+12; with
@@ -1081,6 +1127,7 @@ extern "C" int ff_gemm_s8(const int8_t* A, const int8_t* W, int64_t M, int64_t N
   if (epi == FF_EPI_QKV_ROPE) {
     if (N % 3 != 0 || (N / 3) % 64 != 0) return fail(FF_EINVAL, "gemm_s8: QKV epilogue needs N = 3C with C % 64 == 0");
     if (!rope_cos || !rope_sin || rope_len <= 0) return fail(FF_EINVAL, "gemm_s8: QKV epilogue needs RoPE tables");
+    if (rope_len > (int64_t(1) << 24)) return fail(FF_EINVAL, "gemm_s8: rope_len > 2^24 is not supported");
     if (!aligned(rope_cos, 16) || !aligned(rope_sin, 16)) return fail(FF_EINVAL, "gemm_s8: misaligned RoPE tables");
   }
   if (M == 0) return FF_OK;
