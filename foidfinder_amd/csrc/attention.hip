@@ -22,7 +22,8 @@
 //    fp16 holds at full relative precision and fp32 accumulates far from overflow, so m_ref stays. Otherwise (rare:
 //    the scores rose well above m_ref) m_ref is raised to that half's maximum, O and l are rescaled by
 //    2^(m_old - m_new) and the half's p are recomputed.
-// Tails: query rows >= L are computed on clamped rows and not stored; keys >= L are masked to -inf.
+// Tails: query rows >= L are computed on clamped rows and not stored; keys >= L (zero K rows) get S ~ -2^17 from
+// the same extra MFMA (see one_last below), so their p is exactly 0 with no masking instructions in the loop.
 //
 // Reference: foidfinder/backends/cuda/csrc/attention.cuh:19-157 (which accumulates each 64-key block in fp16 and
 // rescales every block; here every product and sum is fp32).
@@ -146,9 +147,22 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const half_t* __restr
       for (int r = 0; r < 16; ++r) o[qt][dt][r] = 0.f;
   // m_ref enters S through one extra MFMA per accumulator: the row operand `one_k` has 1 in k-slot 0 for every key,
   // the column operand mq[qt] holds -m_ref (fp16) of the lane's query in k-slot 0, so the product starts every
-  // S^T accumulator at -m_ref without a register block per query tile. m_ref is kept fp16-representable.
-  half8_t one_k = {}, mq[2] = {{}, {}};
-  if (fh == 0) one_k[0] = static_cast<half_t>(1.f);
+  // S^T accumulator at -m_ref without a register block per query tile. m_ref is kept fp16-representable (|m_ref| <=
+  // 65000). The last tile uses one_last[kh] instead, which also has 2 in k-slot 1 for keys >= L, against -65504 in
+  // k-slot 1 of mq: those keys start at -m_ref - 131008 < -66000, so exp2 gives exactly 0 (their K rows are zero).
+  // Without a branch or per-score select in the loop (the compiler turns a masked-tile branch into selects on every
+  // tile).
+  half8_t one_k = {}, one_last[2] = {{}, {}}, mq[2] = {{}, {}};
+  if (fh == 0) {
+    one_k[0] = static_cast<half_t>(1.f);
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      one_last[kh][0] = static_cast<half_t>(1.f);
+      one_last[kh][1] = static_cast<half_t>((ntiles - 1) * BKV + kh * 32 + fr >= L ? 2.f : 0.f);
+    }
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) mq[qt][1] = static_cast<half_t>(-65504.f);
+  }
   float m_ref[2] = {0.f, 0.f}, l_run[2] = {0.f, 0.f};
   const half2_t ones = {static_cast<half_t>(1.f), static_cast<half_t>(1.f)};
   auto set_mref = [&](int qt, float m) __attribute__((always_inline)) {
@@ -168,26 +182,15 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const half_t* __restr
 
   auto qk = [&](int kh, int tile, bool last) __attribute__((always_inline)) {
     const float16_t zero = {};
+    const half8_t ok = last ? one_last[kh] : one_k;
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) xs[kh][qt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(one_k, mq[qt], zero, 0, 0, 0);
+    for (int qt = 0; qt < 2; ++qt) xs[kh][qt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ok, mq[qt], zero, 0, 0, 0);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const half8_t kf = *reinterpret_cast<const half8_t*>(smem + ka[s] + kh * 32 * HD);
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt)
         xs[kh][qt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[qt][s], xs[kh][qt], 0, 0, 0);
-    }
-    if (last) {  // keys past the sequence end (their K rows read as zeros)
-      // opaque, so that the 16 comparisons are not hoisted out of the tile loop as 16 live lane masks
-      int lim = L - tile * BKV - kh * 32 - 4 * fh;
-      asm volatile("" : "+v"(lim));
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        if (8 * (r >> 2) + (r & 3) >= lim) {
-          xs[kh][0][r] = -INFINITY;
-          xs[kh][1][r] = -INFINITY;
-        }
-      }
     }
   };
   auto soft = [&](int kh) __attribute__((always_inline)) {
