@@ -1,8 +1,11 @@
-"""ROCm backend: the gfx950 int8 engine behind the reference's Backend protocol.
+"""ROCm backend: the gfx950 int8 engines behind the reference's Backend protocol.
 
 Mirrors CUDABackend (foidfinder/backends/cuda/__init__.py:15-43): constructor (model_dir) raising RuntimeError with
 a readable message when unsupported, `name`, `device`, and `predict(image) -> float32 probabilities [num_tags]`
 (sigmoid applied), called from one thread. Adds `predict_batch(images) -> [B, num_tags]` for batched serving.
+Model directories: PixAI Tagger v1.0 (the reference's own, config.json + model.safetensors with official or
+converted weights), this package's EVA02 int8 taggers (config architecture "eva02-int8"); Haruka directories are
+refused as the reference's CUDA backend refuses them.
 """
 
 from __future__ import annotations
@@ -26,14 +29,17 @@ class ROCmBackend:
         if arch != "gfx950":
             raise RuntimeError(f"ROCm backend: kernels are built for gfx950 (MI355X), found {arch}")
         config = json.loads((Path(model_dir) / "config.json").read_text())
-        arch_name = config.get("model", {}).get("architecture")
-        if arch_name != "eva02-int8":
-            raise RuntimeError(
-                f"ROCm backend runs int8 EVA02 taggers (config architecture 'eva02-int8'), not {arch_name!r}"
-            )
-        from ...engine import load_model_dir
+        arch_name = config.get("model", {}).get("architecture") if isinstance(config.get("model"), dict) else None
+        if arch_name == "eva02-int8":  # this package's EVA02 int8 tagger format
+            from ...engine import load_model_dir
 
-        self.engine, self.config = load_model_dir(model_dir)
+            self.engine, self.config = load_model_dir(model_dir)
+        elif "categories" in config:  # as the reference's CUDA backend (cuda/__init__.py:19-20)
+            raise RuntimeError("Haruka Tagger runs on the MLX backend only")
+        else:  # PixAI Tagger v1.0: official weights or the converted int8 format (cuda/__init__.py:28-31)
+            from ...pixai import load_pixai_dir
+
+            self.engine, self.config = load_pixai_dir(model_dir)
         self.size = self.engine.cfg.img_size
         self.device = torch.cuda.get_device_name()
 

@@ -188,7 +188,90 @@ def synthetic_checkpoint(cfg: Eva02Config, seed: int = 0, head_std: float = 0.05
 GEMMS = ("qkv", "proj", "fc1", "fc2")
 
 
-class Eva02Int8:
+class Int8Engine:
+    """What the int8 engines share (foidfinder/backends/cuda/engine.py:65-184): a per-batch buffer plan, GEMM tile
+    variant autotune, two warm-up forwards on a side stream, graph capture, then replay. Subclasses provide
+    `_buffers(B)`, `_gemm_jobs(buf)` (the four GEMMs of block 0 on those buffers) and `_forward(img, buf, trace)`."""
+
+    device: torch.device
+    variants: dict[tuple[str, int], int]
+    _graphs: dict[int, tuple]
+
+    def _buffers(self, B: int) -> dict[str, torch.Tensor]:
+        raise NotImplementedError
+
+    def _gemm_jobs(self, buf: dict[str, torch.Tensor]) -> dict:
+        raise NotImplementedError
+
+    def _forward(self, img: torch.Tensor, buf: dict[str, torch.Tensor], trace: dict | None = None) -> torch.Tensor:
+        raise NotImplementedError
+
+    def _gemm(self, a, lw, rs, epi, variant, out, rope=None):
+        w, ws, b = lw
+        cos, sin = rope if rope is not None else (None, None)
+        self.k.gemm_s8(a, w, rs, ws, b, out, epi, variant, cos, sin, Q_SCALE)
+
+    def _autotune(self, B: int, buf: dict[str, torch.Tensor]) -> None:
+        """Pick the fastest GEMM tile variant per GEMM for this batch size (engine.py:108-135). The operands are
+        random int8 codes, not zeros: MFMA power and so the clock depend on the data, and zeros would time the
+        variants at a clock that real activations never see."""
+        g = torch.Generator(device=buf["a8"].device).manual_seed(0)
+        for name in ("a8", "h8"):
+            t = buf[name]
+            t.copy_(torch.randint(-127, 128, t.shape, dtype=torch.int8, device=t.device, generator=g))
+        buf["rs"].fill_(1e-2)
+        buf["o16"].zero_()
+        n = lib().ff_gemm_s8_variants()
+        for name, fn in self._gemm_jobs(buf).items():
+            best = None
+            for v in range(1, n + 1):
+                for _ in range(2):
+                    fn(v)
+                start, end = torch.cuda.Event(True), torch.cuda.Event(True)
+                start.record()
+                for _ in range(5):
+                    fn(v)
+                end.record()
+                torch.cuda.synchronize()
+                ms = start.elapsed_time(end)
+                if best is None or ms < best[0]:
+                    best = (ms, v)
+            self.variants[(name, B)] = best[1]
+
+    def eager(self, images: torch.Tensor, trace: dict | None = None) -> torch.Tensor:
+        """One forward without graph capture (fresh buffers)."""
+        buf = self._buffers(images.shape[0])
+        return self._forward(images, buf, trace).clone()
+
+    @torch.no_grad()
+    def __call__(self, images: torch.Tensor) -> torch.Tensor:
+        """images [B, S, S, 3] normalized pixels (any float dtype) -> logits [B, tags] fp32."""
+        B = images.shape[0]
+        if B not in self._graphs:
+            buf = self._buffers(B)
+            self._autotune(B, buf)
+            static_in = torch.zeros(B, *images.shape[1:], device=self.device, dtype=torch.half)
+            stream = torch.cuda.Stream()
+            stream.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(stream):
+                for _ in range(2):  # warm up (library workspaces allocate outside capture)
+                    self._forward(static_in, buf)
+            torch.cuda.current_stream().wait_stream(stream)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                static_out = self._forward(static_in, buf)
+            self._graphs[B] = (graph, static_in, static_out, buf)
+        graph, static_in, static_out, _ = self._graphs[B]
+        static_in.copy_(images)
+        graph.replay()
+        return static_out.clone()
+
+    def replay(self, B: int) -> None:
+        """Replays the captured graph for batch B on its current input (benchmarking)."""
+        self._graphs[B][0].replay()
+
+
+class Eva02Int8(Int8Engine):
     """images [B, S, S, 3] (normalized pixels, NHWC) -> logits [B, tags] fp32, one HIP graph per batch size.
 
     Mirrors PixAICuda (foidfinder/backends/cuda/engine.py:65-184): preallocated buffers, per-batch GEMM variant
@@ -250,11 +333,6 @@ class Eva02Int8:
             "h8": torch.empty(T, hp, device=dev, dtype=torch.int8),
         }
 
-    def _gemm(self, a, lw, rs, epi, variant, out, rope=None):
-        w, ws, b = lw
-        cos, sin = rope if rope is not None else (None, None)
-        self.k.gemm_s8(a, w, rs, ws, b, out, epi, variant, cos, sin, Q_SCALE)
-
     def _gemm_jobs(self, buf):
         lw = self.layers[0]
         return {
@@ -263,33 +341,6 @@ class Eva02Int8:
             "fc1": lambda v: self._gemm(buf["a8"], lw["fc1"], buf["rs"], EPI_SWIGLU, v, buf["h16"]),
             "fc2": lambda v: self._gemm(buf["h8"], lw["fc2"], buf["rs"], EPI_RESIDUAL, v, buf["o16"]),
         }
-
-    def _autotune(self, B: int, buf: dict[str, torch.Tensor]) -> None:
-        """Pick the fastest GEMM tile variant per GEMM for this batch size (engine.py:108-135). The operands are
-        random int8 codes, not zeros: MFMA power and so the clock depend on the data, and zeros would time the
-        variants at a clock that real activations never see."""
-        g = torch.Generator(device=buf["a8"].device).manual_seed(0)
-        for name in ("a8", "h8"):
-            t = buf[name]
-            t.copy_(torch.randint(-127, 128, t.shape, dtype=torch.int8, device=t.device, generator=g))
-        buf["rs"].fill_(1e-2)
-        buf["o16"].zero_()
-        n = lib().ff_gemm_s8_variants()
-        for name, fn in self._gemm_jobs(buf).items():
-            best = None
-            for v in range(1, n + 1):
-                for _ in range(2):
-                    fn(v)
-                start, end = torch.cuda.Event(True), torch.cuda.Event(True)
-                start.record()
-                for _ in range(5):
-                    fn(v)
-                end.record()
-                torch.cuda.synchronize()
-                ms = start.elapsed_time(end)
-                if best is None or ms < best[0]:
-                    best = (ms, v)
-            self.variants[(name, B)] = best[1]
 
     def patchify(self, img: torch.Tensor) -> torch.Tensor:
         """[B, S, S, 3] -> [B * g * g, p*p*3] patches in (kh, kw, c) order, row-major over the grid."""
@@ -330,38 +381,6 @@ class Eva02Int8:
                 trace[f"x{i}"] = x.clone()
         cls = F.layer_norm(xv[:, 0].float(), (d,), *self.norm, eps).half()
         return F.linear(cls, self.head_w, self.head_b).float()
-
-    def eager(self, images: torch.Tensor, trace: dict | None = None) -> torch.Tensor:
-        """One forward without graph capture (fresh buffers)."""
-        buf = self._buffers(images.shape[0])
-        return self._forward(images, buf, trace).clone()
-
-    @torch.no_grad()
-    def __call__(self, images: torch.Tensor) -> torch.Tensor:
-        """images [B, S, S, 3] normalized pixels (any float dtype) -> logits [B, tags] fp32."""
-        B = images.shape[0]
-        if B not in self._graphs:
-            buf = self._buffers(B)
-            self._autotune(B, buf)
-            static_in = torch.zeros(B, *images.shape[1:], device=self.device, dtype=torch.half)
-            stream = torch.cuda.Stream()
-            stream.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(stream):
-                for _ in range(2):  # warm up (library workspaces allocate outside capture)
-                    self._forward(static_in, buf)
-            torch.cuda.current_stream().wait_stream(stream)
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
-                static_out = self._forward(static_in, buf)
-            self._graphs[B] = (graph, static_in, static_out, buf)
-        graph, static_in, static_out, _ = self._graphs[B]
-        static_in.copy_(images)
-        graph.replay()
-        return static_out.clone()
-
-    def replay(self, B: int) -> None:
-        """Replays the captured graph for batch B on its current input (benchmarking)."""
-        self._graphs[B][0].replay()
 
 
 def save_model_dir(out_dir: str | Path, state: dict[str, torch.Tensor], cfg: Eva02Config, tags: list[str],

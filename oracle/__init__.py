@@ -12,6 +12,8 @@ Modules:
   attention  non-causal softmax attention over packed qkv rows, float64
   model      Hadamard matrix, weight quantization/conversion, EVA02 RoPE tables, synthetic EVA02-L/14-448 weights,
              and the int8-semantics forward of the whole tagger
+  pixai      PixAI Tagger v1.0 (the reference's served model): window layout, axial RoPE, stem, attention-pool head,
+             the int8-semantics and float forwards
 
 Pinning (what checks each function beyond restating it) is listed per function in `PINNED`; tests/test_oracle.py
 runs those checks.
@@ -33,4 +35,11 @@ PINNED = {
     "zero-padded columns is zero, residual adds in fp16",
     "attention.attention": "identical keys -> mean of V; one dominant logit -> that V row; shift invariance",
     "model.forward_int8": "agrees with the float forward (no quantization) within the int8 error budget",
+    "pixai.window_perm": "bijection onto the grid; position 0 of window (wr, wc) is grid cell (wr*win, wc*win); "
+    "consecutive positions step one column inside a window row",
+    "pixai.axial_rope64": "row 0 is the identity; explicit angles (column 1 -> 1 rad for pair 0, row 1 for pair 16)",
+    "pixai.patchify": "an image whose patch values encode their grid cell comes out in window_perm order",
+    "pixai.stem": "patch GEMM equals a direct 14x14 stride-14 convolution loop on one patch",
+    "pixai.pool_head": "one-token pooling is the single value row projected; uniform keys -> mean of values",
+    "pixai.forward_int8": "agrees with the float forward (no quantization) within the int8 error budget",
 }
