@@ -1,6 +1,6 @@
 """Throughput of the int8 EVA02-L/14-448 tagger forward on one MI355X, batch 32, HIP-graph replay.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--batch 32] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--batch 32] [--no-cpu-baseline] [--model eva02|pixai]
 
 A step is one forward over a batch of synthetic images (uniform [-1, 1], NHWC fp16, already in HBM) through the
 captured graph: patch-embed GEMM, 24 int8 blocks (3x rotate+quant 1024, rotate+quant h128 + LayerNorm, 4 int8 GEMMs
@@ -37,7 +37,13 @@ def parse():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-images", type=int, default=1, help="images in the CPU baseline sample")
-    return p.parse_args()
+    p.add_argument("--model", choices=("eva02", "pixai"), default="eva02",
+                   help="eva02: the headline EVA02-L/14-448 batch-32 line (default); pixai: PixAI Tagger v1.0 at "
+                        "1008 px, the reference's served model (latency at --batch, default 1)")
+    args = p.parse_args()
+    if args.model == "pixai" and "--batch" not in sys.argv:
+        args.batch = 1
+    return args
 
 
 def timed(fn, stream, iters=20, warm=3) -> float:
@@ -123,12 +129,80 @@ def cpu_baseline(state, cfg, n_images: int) -> dict:
                       f"(numpy oracle, float64 BLAS for the exact int32 GEMMs), {dt:.1f} s"}
 
 
+def bench_pixai(args) -> None:
+    """PixAI Tagger v1.0 at 1008 px (32 blocks, 5184 tokens, windowed + 4 global attention blocks), random-init
+    weights: graph-replay time per batch, and the backend's end-to-end predict (GPU letterbox preprocessing of a
+    1200 x 900 image, forward, sigmoid, copy to the host) at batch 1. The reference publishes 19.8 ms per image for
+    its int8 engine with preprocessing at batch 1 on an RTX 4090 (README.md:173): context, other hardware."""
+    import numpy as np
+    import torch
+    from PIL import Image
+
+    from foidfinder_amd.backends.rocm.preprocess import preprocess
+    from foidfinder_amd.pixai import PixAIConfig, PixAIInt8, convert_checkpoint, synthetic_checkpoint
+
+    dev = torch.device("cuda:0")
+    cfg = PixAIConfig()
+    B = args.batch
+    raw = synthetic_checkpoint(cfg, seed=args.seed)
+    state = convert_checkpoint({k: v.to(dev) for k, v in raw.items()}, cfg)
+    del raw
+    eng = PixAIInt8(state, cfg, device=dev)
+    g = torch.Generator(device="cpu").manual_seed(args.seed + 1)
+    images = (torch.rand(B, cfg.img_size, cfg.img_size, 3, generator=g) * 2 - 1).half().to(dev)
+    assert torch.isfinite(eng(images)).all()
+    for _ in range(args.warmup):
+        eng.replay(B)
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(args.steps):
+        eng.replay(B)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    ms = elapsed / args.steps * 1e3
+    # end to end through the backend's path at batch 1: preprocess + forward + sigmoid + host copy
+    img = Image.fromarray(np.random.default_rng(args.seed).integers(0, 256, (900, 1200, 3), dtype=np.uint8))
+    e2e = []
+    for i in range(args.warmup + args.steps):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        torch.sigmoid(eng(preprocess([img], cfg.img_size))).cpu().numpy()
+        if i >= args.warmup:
+            e2e.append(time.perf_counter() - t)
+    gemm_ops = sum(cfg.gemm_ops(B).values())
+    line = {
+        "metric": "images/sec @1008px int8 PixAI Tagger v1.0 (graph replay)",
+        "value": round(B * args.steps / elapsed, 2),
+        "unit": "images/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "ms_per_image_e2e_batch1": round(1e3 * float(np.median(e2e)), 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "reference_published": {"ms_per_image": 19.8, "hardware": "RTX 4090", "includes": "preprocessing, batch 1"},
+        "dtype": "int8",
+        "data": "synthetic: random-init weights (seeded), images uniform [-1, 1]; e2e: one 1200x900 RGB image",
+        "config": {"workload": "PixAI Tagger v1.0 int8 W8A8 forward, 1008 px, hipGraph replay", "batch": B,
+                   "tokens": cfg.tokens, "window_tokens": cfg.win_tokens, "depth": cfg.depth,
+                   "global_blocks": list(cfg.global_blocks), "hidden": cfg.hidden, "parallelism": "single GPU"},
+        "gemm_variants": {name: eng.variants.get((name, B), 0) for name in ("qkv", "proj", "fc1", "fc2")},
+        "work_per_step": {"gemm_int8_ops": gemm_ops, "attention_flops": cfg.attention_flops(B)},
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}): the tagger forward is data-parallel "
               "over images and every figure here is one GPU's", file=sys.stderr)
         sys.exit(2)
+    if args.model == "pixai":
+        bench_pixai(args)
+        return
     import torch
 
     from foidfinder_amd.engine import Eva02Config, Eva02Int8, convert_checkpoint, synthetic_checkpoint
