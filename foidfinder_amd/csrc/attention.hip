@@ -1,20 +1,21 @@
 // Non-causal flash attention, head_dim 64, fp16 in / fp32 accumulate, on gfx950 fp16 MFMA.
 //
 // Input is the QKV GEMM's output: qkv fp16 [S*L, 3C] with q already rotated and scaled by softmax_scale*log2(e) and
-// k rotated, so the softmax is in base 2. One 256-thread workgroup = 4 waves x 64 queries (two 32-query tiles per
-// wave, so each K/V fragment read from LDS serves 64 queries) of one (sequence, head).
+// k rotated, so the softmax is in base 2. One 256-thread workgroup = 4 waves x 32 queries (one 32-query tile per
+// wave) of one (sequence, head); four workgroups share a CU (16 waves, 4 per SIMD), so one wave's softmax (VALU)
+// runs beside the other waves' MFMA products.
 //
-// K and V stream through a 3-stage LDS ring of 64-key tiles filled by buffer loads straight into LDS
+// K and V stream through a 2-stage LDS ring of 64-key tiles filled by buffer loads straight into LDS
 // (buffer_load_dwordx4 ... lds: no VGPR staging, no LDS write instructions). The buffer descriptor of each tile ends
 // at the sequence's last row, so rows past L read as zeros without any address clamping. Both tiles are stored
 // row-major (64 keys x 128 B); K is read with ds_read_b128 and V with the transposing ds_read_b64_tr_b16, which
 // hands each lane 4 consecutive keys of one d column - the layout the PV MFMA wants - so V is never transposed in
 // software. Rows are XOR-swizzled in 16-byte chunks so that both read patterns are free of bank conflicts.
 //
-// Per wave and 32-query tile, S^T = K Q^T comes from v_mfma_f32_32x32x16_f16 with each lane holding one query and
-// 16 of every 32 keys (the other 16 sit in lane ^ 32), and P^T feeds the PV MFMA (O^T = V^T P^T) directly as its
-// column operand. The tile is processed in two 32-key halves (S, softmax, PV per half). At head_dim 64 the softmax,
-// not the MFMA, bounds the loop, so its common path is one exp2, half a convert and half a dot per score:
+// Per wave, S^T = K Q^T comes from v_mfma_f32_32x32x16_f16 with each lane holding one query and 16 of every 32 keys
+// (the other 16 sit in lane ^ 32), and P^T feeds the PV MFMA (O^T = V^T P^T) directly as its column operand. The
+// tile is processed in two 32-key halves (S, softmax, PV per half). At head_dim 64 the softmax, not the MFMA, bounds
+// the loop, so its common path is one exp2, half a convert and half a dot per score:
 //  * every S^T accumulator starts at -m_ref (the query's reference maximum, kept fp16-representable) through one
 //    extra MFMA whose operands hold 1 and -m_ref in a single k-slot; the first tile sets m_ref to its maximum;
 //  * p = v_exp_f32 (exp2), converted in pairs to fp16; each lane sums its fp16 p with fp32 dot2 (the same p that
@@ -23,7 +24,11 @@
 //    the scores rose well above m_ref) m_ref is raised to that half's maximum, O and l are rescaled by
 //    2^(m_old - m_new) and the half's p are recomputed.
 // Tails: query rows >= L are computed on clamped rows and not stored; keys >= L (zero K rows) get S ~ -2^17 from
-// the same extra MFMA (see one_last below), so their p is exactly 0 with no masking instructions in the loop.
+// the same extra MFMA (see one_last below), so their p is exactly 0 with no masking instructions in the loop; when
+// the last tile's second half holds no key below L it is skipped. The last query block of a sequence, when it holds
+// at most two 32-query units (L = 1025 leaves one query), gives each unit two waves, one per key half, and merges
+// the two partial results through LDS at the end: that block then takes about half a block's time instead of a
+// whole block's with three of its four waves idle.
 //
 // Reference: foidfinder/backends/cuda/csrc/attention.cuh:19-157 (which accumulates each 64-key block in fp16 and
 // rescales every block; here every product and sum is fp32).
@@ -36,14 +41,18 @@ namespace ff {
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int HD = 64;
-constexpr int QW = 64;                // queries per wave
-constexpr int BQ = 4 * QW;            // queries per workgroup
+constexpr int QW = 32;                // queries per wave
+constexpr int WAVES = 4;              // waves per workgroup
+constexpr int BQ = WAVES * QW;        // queries per workgroup
 constexpr int BKV = 64;               // keys per tile
-constexpr int STAGES = 3;             // LDS ring depth
+constexpr int STAGES = 2;             // LDS ring depth
 constexpr int TILE = BKV * HD;        // halves per K (or V) tile: 8 KB
-constexpr int LOADS = 4;              // buffer->LDS loads per thread per tile (2 for K, 2 for V)
+constexpr int KPW = 8 / WAVES;        // 1 KB blocks of each K (and V) tile loaded per wave
+constexpr int LOADS = 2 * KPW;        // buffer->LDS loads per thread per tile
 constexpr float SUM_LIMIT = 8192.f;   // per-lane half-tile sum of p above which m_ref is raised
 constexpr uint32_t RSRC_WORD3 = 0x00020000;  // buffer descriptor word 3: raw dword access (gfx9 family)
+constexpr int MERGE_WORDS = 34;       // floats per lane of a half-1 wave's partial result: O (32), m_ref, l
+static_assert(WAVES / 2 * MERGE_WORDS * 64 * 4 <= 2 * STAGES * TILE * 2, "merge area exceeds the LDS ring");
 
 // Physical 16-byte slot of chunk c in row r. K rows are read 16 rows per ds_read_b128 pass: XOR with bits 1-3 of the
 // row spreads them over all 64 banks. V rows are read by the transposing b64 read, 4 rows x 64 B per 32-lane pass:
@@ -60,18 +69,14 @@ __device__ __forceinline__ void tr_read(half4_t& v, uint32_t lds_addr) {
   asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(lds_addr), "n"(OFF) : "memory");
 }
 
-__global__ __launch_bounds__(256, 2) void attention_kernel(const half_t* __restrict__ qkv, half_t* __restrict__ out,
-                                                           int L, int H) {
-  // K tile of ring slot st at smem + st*TILE, V tile at smem + (STAGES + st)*TILE
-  __shared__ __attribute__((aligned(1024))) half_t smem[2 * STAGES * TILE];
-
+// One workgroup's work. SPLIT = false: wave w owns queries qb*BQ + 32w .. +31 over both key halves of every tile.
+// SPLIT = true (short last block): waves 2u and 2u + 1 share query unit u, each over one key half (kh_sel = w & 1);
+// the half-1 wave's O, m_ref and l are merged into its partner's at the end.
+template <bool SPLIT>
+__device__ __forceinline__ void attention_block(const half_t* __restrict__ qkv, half_t* __restrict__ out, int L,
+                                                int H, int qb, int h, int seq, half_t* smem) {
   const uint32_t smem_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)smem));
   const int C = H * HD, ROW = 3 * C;
-  // 1-D grid over (sequence, head, query block), query block fastest, remapped so that all query blocks of one
-  // (sequence, head) run on one XCD and read its K and V through one L2.
-  const int nq = (L + BQ - 1) / BQ;
-  const int t = xcd_remap(blockIdx.x, gridDim.x);
-  const int qb = t % nq, h = (t / nq) % H, seq = t / (nq * H);
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 31, fh = lane >> 5;
   const int64_t tok0 = static_cast<int64_t>(seq) * L;
@@ -79,34 +84,35 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const half_t* __restr
   const half_t* kbase = qbase + C;
   const half_t* vbase = qbase + 2 * C;
 
-  const int q0 = qb * BQ + wave * QW;
+  const int unit = SPLIT ? wave >> 1 : wave;
+  const int kh_sel = SPLIT ? wave & 1 : 0;
+  const int q0 = qb * BQ + unit * QW;
   const bool active = q0 < L;  // a wave whose queries all lie past L only helps load K and V
-  // Q fragments (column operand of S^T): tile qt, lane holds query q0 + 32qt + fr, d = 16s + 8fh + 0..7.
-  half8_t qf[2][4];
-#pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const int qrow = min(q0 + 32 * qt + fr, L - 1);
+  const int ntiles = (L + BKV - 1) / BKV;
+  const bool h1_empty = (ntiles - 1) * BKV + 32 >= L;  // the last tile's keys 32..63 all lie past L
+
+  // Q fragments (column operand of S^T): lane holds query q0 + fr, d = 16s + 8fh + 0..7.
+  half8_t qf[4];
+  {
+    const int qrow = min(q0 + fr, L - 1);
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      qf[qt][s] = *reinterpret_cast<const half8_t*>(qbase + static_cast<int64_t>(qrow) * ROW + 16 * s + 8 * fh);
+      qf[s] = *reinterpret_cast<const half8_t*>(qbase + static_cast<int64_t>(qrow) * ROW + 16 * s + 8 * fh);
   }
   // Consume Q here, so that the compiler's own wait for these loads is placed once, before the tile loop, and not
   // inside it, where the same vmcnt counter also tracks the tile loads in flight.
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-    for (int s = 0; s < 4; ++s) asm volatile("" ::"v"(qf[qt][s]));
+  for (int s = 0; s < 4; ++s) asm volatile("" ::"v"(qf[s]));
 
-  // Tile loads: wave w fills the 1 KB blocks 2w and 2w + 1 of each tile (rows 8b .. 8b + 7); lane l writes LDS
+  // Tile loads: wave w fills the 1 KB blocks KPW*w .. KPW*w + KPW-1 of each tile (8 rows each); lane l writes LDS
   // slot l of the block, so it fetches the chunk that the swizzle puts there.
-  uint32_t voff_k[2], voff_v[2];
+  uint32_t voff_k[KPW], voff_v[KPW];
 #pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    const int row = 8 * (2 * wave + p) + (lane >> 3), slot = lane & 7;
+  for (int p = 0; p < KPW; ++p) {
+    const int row = 8 * (KPW * wave + p) + (lane >> 3), slot = lane & 7;
     voff_k[p] = static_cast<uint32_t>((row * ROW + k_slot(row, slot) * 8) * 2);
     voff_v[p] = static_cast<uint32_t>((row * ROW + v_slot(row, slot) * 8) * 2);
   }
-  const int ntiles = (L + BKV - 1) / BKV;
   auto issue = [&](int tile) __attribute__((always_inline)) {
     const int st = tile % STAGES;
     const int64_t off = static_cast<int64_t>(tile) * BKV * ROW;
@@ -116,10 +122,10 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const half_t* __restr
     const __amdgpu_buffer_rsrc_t rv =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(vbase + off), 0, nrec, RSRC_WORD3);
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(smem + st * TILE + (2 * wave + p) * 512), 16,
+    for (int p = 0; p < KPW; ++p) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(smem + st * TILE + (KPW * wave + p) * 512), 16,
                                                voff_k[p], 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(smem + (STAGES + st) * TILE + (2 * wave + p) * 512),
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(smem + (STAGES + st) * TILE + (KPW * wave + p) * 512),
                                                16, voff_v[p], 0, 0, 0);
     }
   };
@@ -127,32 +133,30 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const half_t* __restr
   // LDS read offsets (halves, within a tile). K fragment (kh, s): row kh*32 + fr, chunk 2s + fh. V^T fragment
   // (dt, kh, tt), half j: the transposing read over 16-lane groups; lane l of group g addresses row
   // kh*32 + 16tt + 8j + 4fh + (l%16)/4, columns dt*32 + 16(g%2) + 4(l%4) .. +3, and receives 4 consecutive keys of
-  // column dt*32 + fr: MFMA slots 4j .. 4j+3 = keys 16tt + 8j + 4fh + 0..3, the keys of P^T's slots.
+  // column dt*32 + fr: MFMA slots 4j .. 4j+3 = keys 16tt + 8j + 4fh + 0..3, the keys of P^T's slots. A SPLIT wave's
+  // rows start at its own half (kh_sel*32).
   int koff[4], voff[2];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) koff[s] = fr * HD + k_slot(fr, 2 * s + fh) * 8;
+  for (int s = 0; s < 4; ++s) koff[s] = fr * HD + k_slot(fr, 2 * s + fh) * 8 + kh_sel * 32 * HD;
 #pragma unroll
   for (int dt = 0; dt < 2; ++dt) {
     const int row = 4 * fh + ((lane & 15) >> 2);  // + kh*32 + 16tt + 8j, multiples of 4 that leave row & 2 alone
     const int col = dt * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-    voff[dt] = row * HD + v_slot(row, col >> 3) * 8 + (col & 7);
+    voff[dt] = row * HD + v_slot(row, col >> 3) * 8 + (col & 7) + kh_sel * 32 * HD;
   }
 
-  float16_t o[2][2];  // [query tile][d tile]: O^T rows d = 32dt + 8(r/4) + 4fh + r%4, column = the lane's query
+  float16_t o[2];  // [d tile]: O^T rows d = 32dt + 8(r/4) + 4fh + r%4, column = the lane's query
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt)
+  for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[qt][dt][r] = 0.f;
+    for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
   // m_ref enters S through one extra MFMA per accumulator: the row operand `one_k` has 1 in k-slot 0 for every key,
-  // the column operand mq[qt] holds -m_ref (fp16) of the lane's query in k-slot 0, so the product starts every
-  // S^T accumulator at -m_ref without a register block per query tile. m_ref is kept fp16-representable (|m_ref| <=
-  // 65000). The last tile uses one_last[kh] instead, which also has 2 in k-slot 1 for keys >= L, against -65504 in
-  // k-slot 1 of mq: those keys start at -m_ref - 131008 < -66000, so exp2 gives exactly 0 (their K rows are zero).
-  // Without a branch or per-score select in the loop (the compiler turns a masked-tile branch into selects on every
-  // tile).
-  half8_t one_k = {}, one_last[2] = {{}, {}}, mq[2] = {{}, {}};
+  // the column operand mq holds -m_ref (fp16) of the lane's query in k-slot 0, so the product starts every S^T
+  // accumulator at -m_ref. m_ref is kept fp16-representable (|m_ref| <= 65000). The last tile uses one_last[kh]
+  // instead, which also has 2 in k-slot 1 for keys >= L, against -65504 in k-slot 1 of mq: those keys start at
+  // -m_ref - 131008 < -66000, so exp2 gives exactly 0 (their K rows are zero). No branch or per-score select in the
+  // loop (the compiler turns a masked-tile branch into selects on every tile).
+  half8_t one_k = {}, one_last[2] = {{}, {}}, mq = {};
   if (fh == 0) {
     one_k[0] = static_cast<half_t>(1.f);
 #pragma unroll
@@ -160,53 +164,45 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const half_t* __restr
       one_last[kh][0] = static_cast<half_t>(1.f);
       one_last[kh][1] = static_cast<half_t>((ntiles - 1) * BKV + kh * 32 + fr >= L ? 2.f : 0.f);
     }
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) mq[qt][1] = static_cast<half_t>(-65504.f);
+    mq[1] = static_cast<half_t>(-65504.f);
   }
-  float m_ref[2] = {0.f, 0.f}, l_run[2] = {0.f, 0.f};
+  float m_ref = 0.f, l_run = 0.f;
   const half2_t ones = {static_cast<half_t>(1.f), static_cast<half_t>(1.f)};
-  auto set_mref = [&](int qt, float m) __attribute__((always_inline)) {
+  auto set_mref = [&](float m) __attribute__((always_inline)) {
     // smallest fp16 >= m (|m| < 65504): then every p of the tile that set it is <= 1
     const float mc = fminf(fmaxf(m, -65000.f), 65000.f);
     half_t mh = static_cast<half_t>(mc + fabsf(mc) * 0.0009765625f + 6.103515625e-05f);
-    m_ref[qt] = static_cast<float>(mh);
-    if (fh == 0) mq[qt][0] = -mh;
+    m_ref = static_cast<float>(mh);
+    if (fh == 0) mq[0] = -mh;
   };
 
-  // Per tile, the two 32-key halves kh are pipelined: S of half 1 is computed (MFMA) while the softmax of half 0
-  // runs (VALU), and the PV product of half 0 while the softmax of half 1 runs.
-  float16_t xs[2][2];    // [kh][qt]: S^T - m_ref, lane holds keys 32kh + 8(r/4) + 4fh + r%4
-  half8_t pf[2][2][2];   // [kh][qt][tt]: fp16 p, slot u of lane half fh = key 32kh + 16tt + 8(u/4) + 4fh + u%4
-  float hs[2][2];        // [kh][qt]: the lane's sum of its p over half kh
-  int ka[4], va[2];      // this tile's K and V read bases
+  float16_t xs[2];   // [kh]: S^T - m_ref, lane holds keys 32kh + 8(r/4) + 4fh + r%4
+  half8_t pf[2][2];  // [kh][tt]: fp16 p, slot u of lane half fh = key 32kh + 16tt + 8(u/4) + 4fh + u%4
+  float hs[2];       // [kh]: the lane's sum of its p over half kh
+  int ka[4], va[2];  // this tile's K and V read bases
 
-  auto qk = [&](int kh, int tile, bool last) __attribute__((always_inline)) {
+  // Half kh of the tile (SPLIT: slot 0 is the wave's own half, whose rows koff/voff already select)
+  auto qk = [&](int kh, bool last) __attribute__((always_inline)) {
     const float16_t zero = {};
-    const half8_t ok = last ? one_last[kh] : one_k;
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) xs[kh][qt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ok, mq[qt], zero, 0, 0, 0);
+    const half8_t ok = last ? one_last[SPLIT ? kh_sel : kh] : one_k;
+    xs[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ok, mq, zero, 0, 0, 0);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const half8_t kf = *reinterpret_cast<const half8_t*>(smem + ka[s] + kh * 32 * HD);
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt)
-        xs[kh][qt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[qt][s], xs[kh][qt], 0, 0, 0);
+      xs[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], xs[kh], 0, 0, 0);
     }
   };
   auto soft = [&](int kh) __attribute__((always_inline)) {
+    float acc = 0.f;
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      float acc = 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        const half2_t p2 = {static_cast<half_t>(__builtin_amdgcn_exp2f(xs[kh][qt][r])),
-                            static_cast<half_t>(__builtin_amdgcn_exp2f(xs[kh][qt][r + 1]))};
-        acc = __builtin_amdgcn_fdot2(p2, ones, acc, false);
-        pf[kh][qt][r >> 3][r & 7] = p2[0];
-        pf[kh][qt][r >> 3][(r & 7) + 1] = p2[1];
-      }
-      hs[kh][qt] = acc;
+    for (int r = 0; r < 16; r += 2) {
+      const half2_t p2 = {static_cast<half_t>(__builtin_amdgcn_exp2f(xs[kh][r])),
+                          static_cast<half_t>(__builtin_amdgcn_exp2f(xs[kh][r + 1]))};
+      acc = __builtin_amdgcn_fdot2(p2, ones, acc, false);
+      pf[kh][r >> 3][r & 7] = p2[0];
+      pf[kh][r >> 3][(r & 7) + 1] = p2[1];
     }
+    hs[kh] = acc;
   };
   auto pv = [&](auto khc) __attribute__((always_inline)) {
     constexpr int kh = decltype(khc)::value;
@@ -228,37 +224,32 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const half_t* __restr
       for (int tt = 0; tt < 2; ++tt) {
         const half4_t lo = v[dt][tt][0], hi = v[dt][tt][1];
         const half8_t vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt)
-          o[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[kh][qt][tt], o[qt][dt], 0, 0, 0);
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[kh][tt], o[dt], 0, 0, 0);
       }
   };
-  // Lane-pair maximum of xs[kh][qt] (the query's 32 keys of half kh).
-  auto half_max = [&](int kh, int qt) __attribute__((always_inline)) {
-    float v = xs[kh][qt][0];
+  // Lane-pair maximum of xs[kh] (the query's 32 keys of half kh).
+  auto half_max = [&](int kh) __attribute__((always_inline)) {
+    float v = xs[kh][0];
 #pragma unroll
-    for (int r = 1; r < 16; ++r) v = fmaxf(v, xs[kh][qt][r]);
+    for (int r = 1; r < 16; ++r) v = fmaxf(v, xs[kh][r]);
     return fmaxf(v, xor_shuffle(v, 32));
   };
   // Rare path of a half whose p overflowed the limit: raise m_ref to the maximum of S over that half (S recomputed
-  // under the old m_ref), rescale O, l and the sum of half 0 when rescuing half 1, and recompute the S halves whose
-  // softmax is still to come under the new m_ref.
-  auto rescue = [&](int kh, int tile, bool last) __attribute__((always_inline)) {
-    qk(kh, tile, last);
+  // under the old m_ref), rescale O, l and the sum of half 0 when rescuing half 1, and recompute the half's S and p
+  // under the new m_ref.
+  auto rescue = [&](int kh, bool last) __attribute__((always_inline)) {
+    qk(kh, last);
+    const float m_old = m_ref;
+    const float mx = half_max(kh) + m_old;
+    if (mx > m_old) set_mref(mx);
+    const float corr = __builtin_amdgcn_exp2f(m_old - m_ref);
+    l_run *= corr;
+    if (kh == 1) hs[0] *= corr;
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      const float m_old = m_ref[qt];
-      const float mx = half_max(kh, qt) + m_old;
-      if (mx > m_old) set_mref(qt, mx);
-      const float corr = __builtin_amdgcn_exp2f(m_old - m_ref[qt]);
-      l_run[qt] *= corr;
-      if (kh == 1) hs[0][qt] *= corr;
+    for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[qt][dt][r] *= corr;
-    }
-    qk(kh, tile, last);
+      for (int r = 0; r < 16; ++r) o[dt][r] *= corr;
+    qk(kh, last);
     soft(kh);
   };
 
@@ -267,14 +258,15 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const half_t* __restr
     if (j < ntiles) issue(j);
   for (int tile = 0; tile < ntiles; ++tile) {
     // Tile `tile` has landed once at most the loads of the tiles issued after it are outstanding.
-    if (tile + 1 < ntiles)
+    if (tile + 1 < ntiles && STAGES > 2)
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LOADS * (STAGES - 2)) : "memory");
     else
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();  // no fence: the vmcnt wait above already covers this thread's LDS writes
     // The ring slot of tile + STAGES - 1 was last read for tile - 1, which every wave has finished.
     if (tile + STAGES - 1 < ntiles) issue(tile + STAGES - 1);
-    if (!active) continue;
+    const bool last = tile == ntiles - 1;
+    if (!active || (SPLIT && last && kh_sel == 1 && h1_empty)) continue;
     // Read bases, opaque to the compiler so that the fragment offsets fold into the reads' immediate offsets
     // instead of each being precomputed into a register.
     const int st = tile % STAGES;
@@ -291,44 +283,87 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const half_t* __restr
     // One tile (a single copy of the code: per-variant copies of the MFMA regions make the register allocator
     // shuffle the accumulators between them). Each half's p are checked (all lane sums <= SUM_LIMIT) before its PV
     // product; the first tile sets m_ref from its maximum first.
-    const bool last = tile == ntiles - 1;
-    qk(0, tile, last);
+    qk(0, last);
     if (tile == 0) {
-      qk(1, tile, last);
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt) set_mref(qt, fmaxf(half_max(0, qt), half_max(1, qt)));
-      qk(0, tile, last);
+      if constexpr (SPLIT) {
+        set_mref(half_max(0));
+      } else {
+        qk(1, last);
+        set_mref(fmaxf(half_max(0), half_max(1)));
+      }
+      qk(0, last);
     }
     soft(0);
-    if (__any(hs[0][0] > SUM_LIMIT || hs[0][1] > SUM_LIMIT)) rescue(0, tile, last);
+    if (__any(hs[0] > SUM_LIMIT)) rescue(0, last);
     pv(std::integral_constant<int, 0>{});
-    qk(1, tile, last);
-    soft(1);
-    if (__any(hs[1][0] > SUM_LIMIT || hs[1][1] > SUM_LIMIT)) rescue(1, tile, last);
-    pv(std::integral_constant<int, 1>{});
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) l_run[qt] += hs[0][qt] + hs[1][qt];
+    hs[1] = 0.f;
+    if (!SPLIT && !(last && h1_empty)) {
+      qk(1, last);
+      soft(1);
+      if (__any(hs[1] > SUM_LIMIT)) rescue(1, last);
+      pv(std::integral_constant<int, 1>{});
+    }
+    l_run += hs[0] + hs[1];
   }
 
-  if (!active) return;
-#pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const float l_tot = l_run[qt] + xor_shuffle(l_run[qt], 32);
-    const float inv = 1.f / l_tot;
-    const int q = q0 + 32 * qt + fr;
-    if (q < L) {
-      half_t* orow = out + (tok0 + q) * C + h * HD;
+  if constexpr (SPLIT) {
+    // Merge: the half-1 wave of each unit leaves O, m_ref and l (per lane) in the LDS ring, free once every wave has
+    // passed its last tile; a half-1 wave that saw no key (one tile, second half empty) leaves m = -inf.
+    float* comb = reinterpret_cast<float*>(smem) + unit * MERGE_WORDS * 64 + lane;
+    __syncthreads();
+    if (active && kh_sel == 1) {
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          half4_t v;
-#pragma unroll
-          for (int u = 0; u < 4; ++u) v[u] = static_cast<half_t>(o[qt][dt][4 * g + u] * inv);
-          *reinterpret_cast<half4_t*>(orow + dt * 32 + 8 * g + 4 * fh) = v;
-        }
+        for (int r = 0; r < 16; ++r) comb[(dt * 16 + r) * 64] = o[dt][r];
+      comb[32 * 64] = h1_empty && ntiles == 1 ? -__builtin_inff() : m_ref;
+      comb[33 * 64] = l_run;
     }
+    __syncthreads();
+    if (!active || kh_sel == 1) return;
+    const float m1 = comb[32 * 64], l1 = comb[33 * 64];
+    const float m = fmaxf(m_ref, m1);
+    const float c0 = __builtin_amdgcn_exp2f(m_ref - m), c1 = __builtin_amdgcn_exp2f(m1 - m);
+    l_run = l_run * c0 + l1 * c1;
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] * c0 + comb[(dt * 16 + r) * 64] * c1;
+  } else {
+    if (!active) return;
   }
+
+  const float l_tot = l_run + xor_shuffle(l_run, 32);
+  const float inv = 1.f / l_tot;
+  const int q = q0 + fr;
+  if (q < L) {
+    half_t* orow = out + (tok0 + q) * C + h * HD;
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        half4_t v;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = static_cast<half_t>(o[dt][4 * g + u] * inv);
+        *reinterpret_cast<half4_t*>(orow + dt * 32 + 8 * g + 4 * fh) = v;
+      }
+  }
+}
+
+__global__ __launch_bounds__(64 * WAVES, 4) void attention_kernel(const half_t* __restrict__ qkv,
+                                                                  half_t* __restrict__ out, int L, int H) {
+  // K tile of ring slot st at smem + st*TILE, V tile at smem + (STAGES + st)*TILE
+  __shared__ __attribute__((aligned(1024))) half_t smem[2 * STAGES * TILE];
+  // 1-D grid over (sequence, head, query block), query block fastest, remapped so that all query blocks of one
+  // (sequence, head) run on one XCD and read its K and V through one L2.
+  const int nq = (L + BQ - 1) / BQ;
+  const int t = xcd_remap(blockIdx.x, gridDim.x);
+  const int qb = t % nq, h = (t / nq) % H, seq = t / (nq * H);
+  const int units = min(WAVES, (L - qb * BQ + QW - 1) / QW);  // 32-query units of this block
+  if (2 * units <= WAVES)
+    attention_block<true>(qkv, out, L, H, qb, h, seq, smem);
+  else
+    attention_block<false>(qkv, out, L, H, qb, h, seq, smem);
 }
 
 }  // namespace ff
@@ -350,7 +385,8 @@ extern "C" int ff_attention(const void* qkv, void* out, int64_t T, int64_t heads
   const int64_t blocks = (seq_len + BQ - 1) / BQ * heads * seqs;
   if (blocks > 0x7fffffff) return fail(FF_EINVAL, "attention: too many blocks");
   const dim3 grid(static_cast<unsigned>(blocks));
-  attention_kernel<<<grid, 256, 0, as_stream(stream)>>>(static_cast<const half_t*>(qkv), static_cast<half_t*>(out),
-                                                        static_cast<int>(seq_len), static_cast<int>(heads));
+  attention_kernel<<<grid, 64 * WAVES, 0, as_stream(stream)>>>(static_cast<const half_t*>(qkv),
+                                                                static_cast<half_t*>(out), static_cast<int>(seq_len),
+                                                                static_cast<int>(heads));
   return check_launch("attention");
 }

@@ -268,6 +268,19 @@ def test_attention_matches_float64(dev, rng, S, L, H):
     assert np.isfinite(got).all() and err < 4e-3, f"max abs err {err}"
 
 
+# Short last query blocks (at most two 32-query units past the last full 128-query block), whose units are split
+# over two waves by key half and merged: one or two units, the last tile's second key half empty (L mod 64 in
+# 1..32) or not, a single key tile, and PixAI's window (576) and grid (5184) lengths.
+@pytest.mark.parametrize(("S", "L", "H"), [(2, 161, 4), (3, 33, 2), (2, 32, 2), (1, 168, 3), (4, 576, 2),
+                                           (1, 5184, 1), (2, 2, 2), (1, 190, 2)])
+def test_attention_split_tail_blocks(dev, rng, S, L, H):
+    qkv = qkv_inputs(rng, S, L, H)
+    got = run_attention(dev, qkv, L).astype(np.float64)
+    want = OA.attention(qkv, L, out_dtype=np.float64)
+    err = np.abs(got - want).max()
+    assert np.isfinite(got).all() and err < 4e-3, f"max abs err {err}"
+
+
 @pytest.mark.parametrize(("gain", "ramp"), [(8.0, 3.0), (30.0, 0.0), (4.0, 12.0)])
 def test_attention_peaked_and_rising_scores(dev, rng, gain, ramp):
     """Scores of tens to hundreds (base 2) whose maxima grow along the keys: the running maximum must be raised on
