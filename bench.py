@@ -1,6 +1,7 @@
 """Throughput of the int8 EVA02-L/14-448 tagger forward on one MI355X, batch 32, HIP-graph replay.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--batch 32] [--no-cpu-baseline] [--model eva02|pixai]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--batch 32] [--no-cpu-baseline]
+                    [--model eva02|pixai|haruka]
 
 A step is one forward over a batch of synthetic images (uniform [-1, 1], NHWC fp16, already in HBM) through the
 captured graph: patch-embed GEMM, 24 int8 blocks (3x rotate+quant 1024, rotate+quant h128 + LayerNorm, 4 int8 GEMMs
@@ -37,12 +38,13 @@ def parse():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-images", type=int, default=1, help="images in the CPU baseline sample")
-    p.add_argument("--model", choices=("eva02", "pixai"), default="eva02",
+    p.add_argument("--model", choices=("eva02", "pixai", "haruka"), default="eva02",
                    help="eva02: the headline EVA02-L/14-448 batch-32 line (default); pixai: PixAI Tagger v1.0 at "
-                        "1008 px, the reference's served model (latency at --batch, default 1)")
+                        "1008 px, the reference's served model (latency at --batch, default 1); haruka: Haruka "
+                        "Tagger, EVA02-B/14-448 + tree pool + 98782-tag head (--batch default 64)")
     args = p.parse_args()
-    if args.model == "pixai" and "--batch" not in sys.argv:
-        args.batch = 1
+    if "--batch" not in sys.argv:
+        args.batch = {"pixai": 1, "haruka": 64}.get(args.model, args.batch)
     return args
 
 
@@ -194,6 +196,129 @@ def bench_pixai(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+def kernel_row(us: float, bound: str, work: int, per_fwd: int) -> dict:
+    if bound == "hbm":
+        ach, peak, unit = work / us / 1e3, PEAK_HBM_GBS, "GB/s"
+    elif bound == "mfma_int8":
+        ach, peak, unit = work / us / 1e6, PEAK_INT8_TOPS, "TFLOP/s"
+    else:
+        ach, peak, unit = work / us / 1e6, PEAK_FP16_TFLOPS, "TFLOP/s"
+    return {"us": round(us, 2), "launches_per_step": per_fwd, "work_per_launch": work, "achieved": round(ach, 1),
+            "unit": unit, "peak": peak, "frac": round(ach / peak, 4), "bound": "hbm" if bound == "hbm" else "mfma"}
+
+
+def bench_haruka(args) -> None:
+    """Haruka Tagger (EVA02-B/14 at 448 px, 12 int8 blocks of d 768, tree pool, 1152 -> 98782 head), random-init
+    weights in the reference's folded format, converted to int8 on load: graph-replay time per batch (raw uint8
+    pixels already in HBM), each block kernel and the pool head timed alone on the graph's buffers, and the
+    backend's end-to-end predict of one 1200 x 900 image (model-card letterbox on the host, forward, sigmoid, copy
+    back) at batch 1. The reference serves Haruka on Apple GPUs only and publishes no number for it."""
+    import numpy as np
+    import torch
+    from PIL import Image
+
+    from foidfinder_amd.backends.rocm.preprocess import preprocess_haruka
+    from foidfinder_amd.haruka import HarukaConfig, HarukaInt8, convert_checkpoint, synthetic_checkpoint
+    from foidfinder_amd.kernels import EPI_QKV_ROPE, EPI_RESIDUAL, EPI_SWIGLU
+
+    dev = torch.device("cuda:0")
+    cfg = HarukaConfig()
+    B = args.batch
+    t0 = time.perf_counter()
+    raw = synthetic_checkpoint(cfg, seed=args.seed)
+    state = convert_checkpoint({k: v.to(dev) for k, v in raw.items()}, cfg)
+    del raw
+    eng = HarukaInt8(state, cfg, device=dev)
+    g = torch.Generator(device="cpu").manual_seed(args.seed + 1)
+    images = torch.randint(0, 256, (B, cfg.img_size, cfg.img_size, 3), generator=g, dtype=torch.uint8).to(dev)
+    assert torch.isfinite(eng(images)).all()
+    torch.cuda.synchronize()
+    print(f"setup {time.perf_counter() - t0:.1f}s; variants { {k[0]: v for k, v in eng.variants.items()} }",
+          file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        eng.replay(B)
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(args.steps):
+        eng.replay(B)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    ms = elapsed / args.steps * 1e3
+    ips = B * args.steps / elapsed
+    print(f"{ips:.1f} images/s, {ms:.2f} ms per batch of {B}", file=sys.stderr, flush=True)
+
+    buf = eng._graphs[B][3]
+    k, lw, st = eng.k, eng.layers[0], torch.cuda.current_stream()
+    M, d, h, L = B * cfg.tokens, cfg.dim, cfg.hidden, cfg.tokens
+    v = {n: eng.variants.get((n, B), 0) for n in ("qkv", "proj", "fc1", "fc2")}
+    x2 = buf["x"].clone()
+    xn = torch.nn.functional.layer_norm(buf["x"].view(B, L, d), (d,), *eng.norm, cfg.eps)
+    jobs = {
+        "rot_q8_h128_ln_768": (lambda: k.rot_q8_h128(buf["x"], buf["a8"], buf["rs"], *lw["n1"], d, cfg.eps),
+                               "hbm", M * d * 3 + 4 * M + 8 * d, 2 * cfg.depth),
+        "rot_q8_h128_768": (lambda: k.rot_q8_h128(buf["o16"], buf["a8"], buf["rs"]), "hbm", M * d * 3 + 4 * M,
+                            cfg.depth),
+        "rot_q8_h128_ln_2048": (lambda: k.rot_q8_h128(buf["h16"], buf["h8"], buf["rs"], *lw["nm"], h, cfg.eps),
+                                "hbm", M * h * 3 + 4 * M + 8 * h, cfg.depth),
+        "gemm_qkv": (lambda: eng._gemm(buf["a8"], lw["qkv"], buf["rs"], EPI_QKV_ROPE, v["qkv"], buf["qkv"], eng.rope),
+                     "mfma_int8", 2 * M * 3 * d * d, cfg.depth),
+        "gemm_proj": (lambda: eng._gemm(buf["a8"], lw["proj"], buf["rs"], EPI_RESIDUAL, v["proj"], x2),
+                      "mfma_int8", 2 * M * d * d, cfg.depth),
+        "gemm_fc1": (lambda: eng._gemm(buf["a8"], lw["fc1"], buf["rs"], EPI_SWIGLU, v["fc1"], buf["h16"]),
+                     "mfma_int8", 2 * M * 2 * h * d, cfg.depth),
+        "gemm_fc2": (lambda: eng._gemm(buf["h8"], lw["fc2"], buf["rs"], EPI_RESIDUAL, v["fc2"], x2),
+                     "mfma_int8", 2 * M * d * h, cfg.depth),
+        "attention": (lambda: k.attention(buf["qkv"], buf["o16"], L), "mfma_fp16", 4 * B * cfg.heads * L * L * 64,
+                      cfg.depth),
+        # the head GEMM's fp16 weights dominate the pool head's bytes
+        "pool_head": (lambda: eng.pool_head(xn), "hbm", cfg.tags * cfg.leaves * cfg.leaf_dim * 2, 1),
+    }
+    kern = {name: kernel_row(timed(fn, st), bound, work, n) for name, (fn, bound, work, n) in jobs.items()}
+    for n, r in kern.items():
+        print(f"  {n:20s} {r['us']:8.1f} us x{r['launches_per_step']:3d}  {r['achieved']:8.1f} {r['unit']}"
+              f"  ({100 * r['frac']:.1f}% of peak)", file=sys.stderr, flush=True)
+    per_step = {n: r["us"] * r["launches_per_step"] for n, r in kern.items()}
+    dom = max(per_step, key=per_step.get)
+    gemm = [n for n in kern if n.startswith("gemm_")]
+    gemm_tops = sum(kern[n]["work_per_launch"] * kern[n]["launches_per_step"] for n in gemm) / sum(
+        per_step[n] for n in gemm) / 1e6
+    img = Image.fromarray(np.random.default_rng(args.seed).integers(0, 256, (900, 1200, 3), dtype=np.uint8))
+    e2e = []
+    for i in range(args.warmup + args.steps):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        torch.sigmoid(eng(preprocess_haruka([img], cfg.img_size))).cpu().numpy()
+        if i >= args.warmup:
+            e2e.append(time.perf_counter() - t)
+    line = {
+        "metric": "images/sec @448px int8 Haruka Tagger (EVA02-B/14 + tree pool, 98782 tags)",
+        "value": round(ips, 2),
+        "unit": "images/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "ms_per_image_e2e_batch1": round(1e3 * float(np.median(e2e)), 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic: random-init weights (seeded, folded format), raw pixels uniform 0..255 (uint8); "
+                "e2e: one 1200x900 RGB image",
+        "config": {"workload": "Haruka Tagger int8 W8A8 forward, 448 px, hipGraph replay", "batch": B,
+                   "seq_len": cfg.tokens, "dim": cfg.dim, "depth": cfg.depth, "heads": cfg.heads,
+                   "mlp_hidden": cfg.hidden, "pool": f"{cfg.coarse} coarse + {cfg.leaves} leaf queries, "
+                   f"{cfg.pool_heads} heads", "tags": cfg.tags, "parallelism": "single GPU"},
+        "gemm_tops": round(gemm_tops, 1),
+        "gemm_frac_of_int8_peak": round(gemm_tops / PEAK_INT8_TOPS, 4),
+        "roofline": {"kernel": dom, **{f: kern[dom][f] for f in ("bound", "achieved", "peak", "unit", "frac")}},
+        "kernels": kern,
+        "gemm_variants": v,
+        "work_per_step": {"gemm_int8_ops": sum(cfg.gemm_ops(B).values()), "attention_flops": cfg.attention_flops(B)},
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -202,6 +327,9 @@ def main():
         sys.exit(2)
     if args.model == "pixai":
         bench_pixai(args)
+        return
+    if args.model == "haruka":
+        bench_haruka(args)
         return
     import torch
 

@@ -4,8 +4,9 @@ Mirrors CUDABackend (foidfinder/backends/cuda/__init__.py:15-43): constructor (m
 a readable message when unsupported, `name`, `device`, and `predict(image) -> float32 probabilities [num_tags]`
 (sigmoid applied), called from one thread. Adds `predict_batch(images) -> [B, num_tags]` for batched serving.
 Model directories: PixAI Tagger v1.0 (the reference's own, config.json + model.safetensors with official or
-converted weights), this package's EVA02 int8 taggers (config architecture "eva02-int8"); Haruka directories are
-refused as the reference's CUDA backend refuses them.
+converted weights), Haruka Tagger (config architecture "haruka-eva02-tree", the folded or compressed checkpoint that
+foidfinder/haruka.py and haruka_quant.py write; the reference serves it on MLX only), and this package's EVA02 int8
+taggers (config architecture "eva02-int8").
 """
 
 from __future__ import annotations
@@ -16,7 +17,7 @@ from pathlib import Path
 import numpy as np
 import torch
 
-from .preprocess import preprocess
+from .preprocess import preprocess, preprocess_haruka
 
 
 class ROCmBackend:
@@ -30,12 +31,18 @@ class ROCmBackend:
             raise RuntimeError(f"ROCm backend: kernels are built for gfx950 (MI355X), found {arch}")
         config = json.loads((Path(model_dir) / "config.json").read_text())
         arch_name = config.get("model", {}).get("architecture") if isinstance(config.get("model"), dict) else None
+        self._preprocess = preprocess
         if arch_name == "eva02-int8":  # this package's EVA02 int8 tagger format
             from ...engine import load_model_dir
 
             self.engine, self.config = load_model_dir(model_dir)
-        elif "categories" in config:  # as the reference's CUDA backend (cuda/__init__.py:19-20)
-            raise RuntimeError("Haruka Tagger runs on the MLX backend only")
+        elif arch_name == "haruka-eva02-tree":  # as the MLX backend selects it (mlx/__init__.py:22-23)
+            from ...haruka import load_haruka_dir
+
+            self.engine, self.config = load_haruka_dir(model_dir)
+            self._preprocess = preprocess_haruka
+        elif "categories" in config:
+            raise RuntimeError(f"ROCm backend: unsupported model architecture {arch_name!r}")
         else:  # PixAI Tagger v1.0: official weights or the converted int8 format (cuda/__init__.py:28-31)
             from ...pixai import load_pixai_dir
 
@@ -49,5 +56,5 @@ class ROCmBackend:
 
     @torch.no_grad()
     def predict_batch(self, images: list) -> np.ndarray:
-        logits = self.engine(preprocess(images, self.size))
+        logits = self.engine(self._preprocess(images, self.size))
         return torch.sigmoid(logits).cpu().numpy()

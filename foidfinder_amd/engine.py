@@ -196,6 +196,7 @@ class Int8Engine:
     device: torch.device
     variants: dict[tuple[str, int], int]
     _graphs: dict[int, tuple]
+    q_scale: float = Q_SCALE  # factor on q after RoPE in the QKV epilogue: softmax scale (unless folded) x log2(e)
 
     def _buffers(self, B: int) -> dict[str, torch.Tensor]:
         raise NotImplementedError
@@ -209,7 +210,7 @@ class Int8Engine:
     def _gemm(self, a, lw, rs, epi, variant, out, rope=None):
         w, ws, b = lw
         cos, sin = rope if rope is not None else (None, None)
-        self.k.gemm_s8(a, w, rs, ws, b, out, epi, variant, cos, sin, Q_SCALE)
+        self.k.gemm_s8(a, w, rs, ws, b, out, epi, variant, cos, sin, self.q_scale)
 
     def _autotune(self, B: int, buf: dict[str, torch.Tensor]) -> None:
         """Pick the fastest GEMM tile variant per GEMM for this batch size (engine.py:108-135). The operands are

@@ -14,6 +14,8 @@ Modules:
              and the int8-semantics forward of the whole tagger
   pixai      PixAI Tagger v1.0 (the reference's served model): window layout, axial RoPE, stem, attention-pool head,
              the int8-semantics and float forwards
+  haruka     Haruka Tagger (EVA02-B + slot-sigmoid tree pool): weight conversion, stem, tree-pool head, the
+             int8-semantics and float forwards
 
 Pinning (what checks each function beyond restating it) is listed per function in `PINNED`; tests/test_oracle.py
 runs those checks.
@@ -42,4 +44,9 @@ PINNED = {
     "pixai.stem": "patch GEMM equals a direct 14x14 stride-14 convolution loop on one patch",
     "pixai.pool_head": "one-token pooling is the single value row projected; uniform keys -> mean of values",
     "pixai.forward_int8": "agrees with the float forward (no quantization) within the int8 error budget",
+    "haruka.convert_checkpoint": "dequantized fc1 rows times H128 give back the gate and value rows, interleaved",
+    "haruka.stem": "token 0 is cls; a patch token equals a direct 14x14 convolution sum plus its bias",
+    "haruka.pool_head": "equals the model card's MHAttnPool (unfolded key scale, child queries broadcast per coarse "
+    "query, einsum leaves) in float64 torch",
+    "haruka.forward_int8": "agrees with the float forward (no quantization) within the int8 error budget",
 }

@@ -1,0 +1,213 @@
+"""The Haruka int8 engine on the GPU against the CPU oracle, same converted weights, on a model of Haruka's structure
+at a small size (112 px: 1 cls + 8 x 8 tokens, d 768, hidden 256, 64 tags).
+
+Bars, as for the EVA02 engine (tests/test_engine_gpu.py): (1) wiring bit-exact under teacher forcing at the
+attention and SwiGLU outputs (qkv and every block output reproduced bit for bit; the SwiGLU output within 2e-3 of
+the oracle's), with each block's attention within 4e-3 of float64 attention; the tree-pool head on the engine's
+final stream within 3e-3 in probability; (2) end to end within 1.5x the int8 noise budget; (3) graph replay equal to
+eager.
+"""
+
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+
+from oracle import attention as OA
+from oracle import haruka as OH
+from oracle import model as OM
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+def cfgs(depth=2, **kw):
+    from foidfinder_amd.haruka import HarukaConfig
+
+    kw = {**dict(img_size=112, depth=depth, hidden=256, tags=64), **kw}
+    return HarukaConfig(**kw), OH.HarukaConfig(**kw)
+
+
+def model(cfg, seed=0):
+    from foidfinder_amd.haruka import convert_checkpoint, synthetic_checkpoint
+
+    raw = synthetic_checkpoint(cfg, seed=seed)
+    return raw, convert_checkpoint(raw, cfg)
+
+
+def pixels(n, cfg, seed):
+    return np.random.default_rng(seed).integers(0, 256, (n, cfg.img_size, cfg.img_size, 3), dtype=np.uint8)
+
+
+def test_haruka_wiring_bit_exact(dev):
+    from foidfinder_amd.haruka import HarukaInt8
+
+    cfg, ocfg = cfgs(depth=3)
+    _, state = model(cfg)
+    eng = HarukaInt8(state, cfg, device=dev)
+    img = pixels(2, cfg, seed=1)
+    trace = {}
+    logits = eng.eager(torch.from_numpy(img).to(dev), trace).cpu().numpy()
+    st = {k: v.numpy() for k, v in state.items()}
+    rope = tuple(t.cpu().numpy() for t in eng.rope)
+    want_rope = OM.eva02_rope_tables(cfg.grid, cfg.rope_ref)
+    assert all(np.array_equal(a, b) for a, b in zip(rope, want_rope)), "rope tables"
+    x = trace["stem"].cpu().numpy()
+    want_stem = OH.stem(img, st, ocfg).astype(np.float32)
+    assert np.abs(x.astype(np.float32) - want_stem).max() <= 4e-3 * max(1.0, np.abs(want_stem).max()), "stem"
+    worst_attn = 0.0
+    for i in range(cfg.depth):
+        rec = {}
+        o_eng, h_eng = trace[f"attn{i}"].cpu().numpy(), trace[f"h{i}"].cpu().numpy()
+        x_new = OH.block_int8(x, st, i, ocfg, rope, attention_out=o_eng, hidden_out=h_eng, record=rec)
+        qkv_eng = trace[f"qkv{i}"].cpu().numpy()
+        assert np.array_equal(rec["qkv"].view(np.uint16), qkv_eng.view(np.uint16)), f"block {i}: qkv differs"
+        h_err = np.abs(h_eng.astype(np.float32) - rec["h"].astype(np.float32)).max()
+        assert h_err <= 2e-3, f"block {i}: SwiGLU output off by {h_err}"
+        x_eng = trace[f"x{i}"].cpu().numpy()
+        assert np.array_equal(x_new.view(np.uint16), x_eng.view(np.uint16)), f"block {i}: block output differs"
+        o_want = OA.attention(qkv_eng, cfg.tokens, out_dtype=np.float64)
+        worst_attn = max(worst_attn, float(np.abs(o_eng.astype(np.float64) - o_want).max()))
+        x = x_eng
+    assert worst_attn < 4e-3, f"attention max abs err {worst_attn}"
+    want = OH.head(x, st, ocfg)
+    p, pw = 1 / (1 + np.exp(-logits.astype(np.float64))), 1 / (1 + np.exp(-want))
+    assert np.abs(p - pw).max() < 3e-3, f"tree-pool head off by {np.abs(p - pw).max()}"
+
+
+def test_haruka_end_to_end_within_int8_noise(dev):
+    from foidfinder_amd.haruka import HarukaInt8
+
+    cfg, ocfg = cfgs(depth=2)
+    raw, state = model(cfg, seed=2)
+    img = pixels(2, cfg, seed=3)
+    eng = HarukaInt8(state, cfg, device=dev)
+    logits = eng.eager(torch.from_numpy(img).to(dev)).cpu().numpy().astype(np.float64)
+    assert np.isfinite(logits).all()
+    p = 1 / (1 + np.exp(-logits))
+    p8 = OH.forward_int8(img, {k: v.numpy() for k, v in state.items()}, ocfg)
+    pf = OH.forward_float(img, {k: v.numpy() for k, v in raw.items()}, ocfg)
+    err, budget = np.abs(p - p8), np.abs(p8 - pf)
+    print(f"engine vs oracle int8: max {err.max():.3e} mean {err.mean():.3e}; "
+          f"oracle int8 vs float: max {budget.max():.3e} mean {budget.mean():.3e}", flush=True)
+    assert err.max() <= 1.5 * budget.max() and err.mean() <= 1.5 * budget.mean()
+
+
+def test_haruka_graph_replay_matches_eager(dev):
+    from foidfinder_amd.haruka import HarukaInt8
+
+    cfg, _ = cfgs(depth=2)
+    eng = HarukaInt8(model(cfg, seed=4)[1], cfg, device=dev)
+    a = torch.from_numpy(pixels(3, cfg, seed=5)).to(dev)
+    b = torch.from_numpy(pixels(3, cfg, seed=6)).to(dev)
+    ea, eb = eng.eager(a), eng.eager(b)
+    for i in range(4):
+        x = a if i % 2 == 0 else b
+        got = eng(x)
+        torch.cuda.synchronize()
+        want = ea if i % 2 == 0 else eb
+        assert torch.equal(got, want), f"replay {i} differs from eager"
+        eng.eager(b)
+        torch.cuda.synchronize()
+
+
+def test_haruka_full_size_block_runs(dev):
+    """Two blocks at Haruka's real size, 448 px, batch 1: 1025 tokens, d 768 (6 rotation blocks of 128), 12 heads,
+    hidden 2048; qkv and block outputs bit-exact with the oracle on the engine's own inputs, finite logits."""
+    from foidfinder_amd.haruka import HarukaConfig, HarukaInt8, convert_checkpoint, synthetic_checkpoint
+
+    cfg = HarukaConfig(depth=2, tags=256)
+    ocfg = OH.HarukaConfig(depth=2, tags=256)
+    state = convert_checkpoint(synthetic_checkpoint(cfg, seed=7), cfg)
+    eng = HarukaInt8(state, cfg, device=dev)
+    img = pixels(1, cfg, seed=8)
+    trace = {}
+    logits = eng.eager(torch.from_numpy(img).to(dev), trace)
+    assert torch.isfinite(logits).all()
+    st = {k: v.numpy() for k, v in state.items()}
+    rope = tuple(t.cpu().numpy() for t in eng.rope)
+    x = trace["stem"].cpu().numpy()
+    for i in range(cfg.depth):
+        rec = {}
+        x_new = OH.block_int8(x, st, i, ocfg, rope, attention_out=trace[f"attn{i}"].cpu().numpy(),
+                              hidden_out=trace[f"h{i}"].cpu().numpy(), record=rec)
+        assert np.array_equal(rec["qkv"].view(np.uint16), trace[f"qkv{i}"].cpu().numpy().view(np.uint16))
+        assert np.array_equal(x_new.view(np.uint16), trace[f"x{i}"].cpu().numpy().view(np.uint16))
+        x = trace[f"x{i}"].cpu().numpy()
+
+
+def write_folded_dir(path, cfg, seed):
+    """A Haruka model directory as foidfinder/haruka.py:convert writes it: fp16 folded tensors + config.json."""
+    from safetensors.torch import save_file
+
+    from foidfinder_amd.haruka import synthetic_checkpoint
+
+    sd = synthetic_checkpoint(cfg, seed=seed)
+    save_file({k: v.half().contiguous() for k, v in sd.items()}, str(path / "model.safetensors"))
+    model = {"name": "Haruka Tagger", "architecture": "haruka-eva02-tree", "img_size": cfg.img_size,
+             "patch_size": cfg.patch, "dim": cfg.dim, "heads": cfg.heads, "depth": cfg.depth,
+             "mlp_hidden": cfg.hidden, "pool_heads": cfg.pool_heads, "coarse_queries": cfg.coarse,
+             "leaf_queries": cfg.leaves, "leaf_dim": cfg.leaf_dim, "rope_ref_grid": cfg.rope_ref}
+    tags = [f"t{i}" for i in range(cfg.tags)]
+    (path / "config.json").write_text(json.dumps({"model": model, "tags": tags, "categories": ["general"] * cfg.tags,
+                                                  "thresholds": {"general": 0.35}}))
+    return sd, model, tags
+
+
+def test_rocm_backend_serves_haruka_model_dirs(dev, tmp_path):
+    """Folded (foidfinder/haruka.py:convert) and compressed (foidfinder/haruka_quant.py) Haruka directories load
+    through backends.load("rocm", dir); predict(image) -> float32 probabilities [num_tags] after the model card's
+    letterbox; the compressed directory, rebuilt from the same codes, predicts what its folded twin predicts."""
+    import gzip
+
+    from PIL import Image
+    from safetensors.numpy import save_file
+
+    from foidfinder_amd import backends
+
+    cfg, _ = cfgs(depth=2)
+    folded = tmp_path / "folded"
+    folded.mkdir()
+    sd, model_entry, tags = write_folded_dir(folded, cfg, seed=9)
+    be = backends.load("rocm", folded)
+    assert be.name == "rocm" and be.size == cfg.img_size
+    rng = np.random.default_rng(10)
+    img = Image.fromarray(rng.integers(0, 256, (90, 140, 3), dtype=np.uint8))
+    p = be.predict(img)
+    assert p.shape == (cfg.tags,) and p.dtype == np.float32 and ((p > 0) & (p < 1)).all()
+    pb = be.predict_batch([img, img.convert("L").convert("RGB"), img])
+    assert pb.shape == (3, cfg.tags) and np.array_equal(pb[0], pb[2])
+
+    # compressed twin: the head and block-0 qkv as row steps x codes; the same matrices go into a folded twin
+    comp, twin = tmp_path / "compressed", tmp_path / "twin"
+    comp.mkdir()
+    twin.mkdir()
+    tensors, layers, twin_sd = {}, {}, {k: v.half() for k, v in sd.items()}
+    for k in ("head.weight", "blocks.0.qkv.weight"):
+        w = sd[k].double().numpy()
+        step = (np.sqrt((w**2).mean(1)) / 32).astype(np.float16)
+        codes = np.rint(w / step.astype(np.float64)[:, None]).astype(np.int64)
+        z = np.where(codes >= 0, 2 * codes, -2 * codes - 1).astype(np.uint64)
+        n = max(1, (int(z.max()).bit_length() + 7) // 8)
+        for i in range(n):
+            tensors[f"{k}.plane{i}"] = np.frombuffer(
+                gzip.compress(((z >> np.uint64(8 * i)) & np.uint64(0xFF)).astype(np.uint8).tobytes()), np.uint8)
+        tensors[k + ".step"] = step
+        layers[k] = {"shape": list(w.shape), "planes": n}
+        twin_sd[k] = torch.from_numpy((codes * step.astype(np.float32)[:, None].astype(np.float64)).astype(np.float32))
+    for k, v in sd.items():
+        if k not in layers:
+            tensors[k] = v.half().numpy()
+    save_file(tensors, str(comp / "model.safetensors"), {"format": "foidfinder-haruka-rowstep1"})
+    config = {"model": model_entry, "quantization": {"format": "foidfinder-haruka-rowstep1", "layers": layers},
+              "tags": tags, "categories": ["general"] * cfg.tags, "thresholds": {"general": 0.35}}
+    (comp / "config.json").write_text(json.dumps(config))
+    from safetensors.torch import save_file as save_torch
+
+    save_torch({k: v.contiguous() for k, v in twin_sd.items()}, str(twin / "model.safetensors"))
+    (twin / "config.json").write_text(json.dumps({k: v for k, v in config.items() if k != "quantization"}))
+    pc = backends.load("rocm", comp).predict(img)
+    pt = backends.load("rocm", twin).predict(img)
+    assert np.array_equal(pc, pt)

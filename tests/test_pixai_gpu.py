@@ -139,7 +139,8 @@ def test_pixai_full_size_block_runs(dev):
 
 def test_rocm_backend_serves_a_pixai_model_dir(dev, tmp_path):
     """The reference's model-directory contract (config.json + model.safetensors with official weights, converted
-    on load): backends.load("rocm", dir).predict(image) -> probabilities; Haruka directories are refused."""
+    on load): backends.load("rocm", dir).predict(image) -> probabilities; tag directories of an unknown
+    architecture are refused."""
     import json
 
     from PIL import Image
@@ -161,8 +162,9 @@ def test_rocm_backend_serves_a_pixai_model_dir(dev, tmp_path):
     pb = be.predict_batch([img, img.convert("L").convert("RGB"), img])
     assert pb.shape == (3, cfg.tags) and np.array_equal(pb[0], pb[2])
     assert np.abs(pb[0] - p).max() < 0.05  # batch 1 and 3 differ only through the fp16 stem GEMM's blocking
-    haruka = tmp_path / "haruka"
-    haruka.mkdir()
-    (haruka / "config.json").write_text(json.dumps({"categories": ["general"], "tags": ["a"]}))
-    with pytest.raises(RuntimeError, match="MLX"):
-        backends.load("rocm", haruka)
+    other = tmp_path / "other"
+    other.mkdir()
+    (other / "config.json").write_text(json.dumps({"model": {"architecture": "vit-x"}, "categories": ["general"],
+                                                   "tags": ["a"]}))
+    with pytest.raises(RuntimeError, match="unsupported model architecture"):
+        backends.load("rocm", other)
