@@ -240,8 +240,19 @@ class HarukaInt8(Int8Engine):
         # tree pool (mlx/haruka.py:104-136)
         self.pool = {name: (half(t[f"pool.{name}.weight"]), half(t[f"pool.{name}.bias"]))
                      for name in ("norm", "trunk_norm", "child_q_norm", "leaf_norm")}
-        self.pool_kv = (half(t["pool.kv.weight"]), half(t["pool.kv.bias"]))
-        self.q_coarse = half(t["pool.q_coarse"].reshape(cfg.coarse, d))
+        # Keys and values are never formed: per pool head h, a query's logit against token x is
+        # x . (Wk_h^T q) + q . bk_h, and its pooled value is Wv_h (sum_n a_n x_n) + bv_h sum_n a_n. The coarse queries
+        # are weights, so their Wk_h^T q columns are precomputed (float64, rounded once).
+        Hp, hd, C = cfg.pool_heads, d // cfg.pool_heads, cfg.coarse
+        kv_w, kv_b = t["pool.kv.weight"].double(), t["pool.kv.bias"].double()
+        wk, bk = kv_w[:d].reshape(Hp, hd, d), kv_b[:d].reshape(Hp, hd)
+        qc = t["pool.q_coarse"].double().reshape(C, Hp, hd)
+        self.coarse_uT = half(torch.einsum("hed,mhe->dhm", wk, qc).reshape(d, Hp * C))  # column h*C + m
+        self.coarse_c = torch.einsum("he,mhe->hm", bk, qc).reshape(Hp * C).float().contiguous()
+        self.pool_kT = half(wk.transpose(1, 2))  # [Hp, d, hd]: Wk_h^T
+        self.pool_bk = bk.float().contiguous()
+        self.pool_vT = half(kv_w[d:].reshape(Hp, hd, d).transpose(1, 2))  # [Hp, d, hd]: Wv_h^T
+        self.pool_bv = kv_b[d:].reshape(Hp, hd).float().contiguous()
         self.q_coarse_bias = t["pool.q_coarse_bias"].float().reshape(cfg.coarse).contiguous()
         self.q_child = half(t["pool.q_child"].reshape(cfg.leaves, d))
         self.q_child_bias = t["pool.q_child_bias"].float().reshape(cfg.leaves).contiguous()
@@ -285,9 +296,14 @@ class HarukaInt8(Int8Engine):
         return x.reshape(B * g * g, p * p * 3)
 
     def pool_head(self, x: torch.Tensor) -> torch.Tensor:
-        """Tree attention pool over the normalized tokens x [B, N, d] fp16 -> logits [B, tags] fp32
-        (mlx/haruka.py:104-136): queries compete per token (softmax over queries) and each token is also gated by
-        sigmoid(logit + bias); 6 coarse queries feed 3 leaf queries each; leaves are weighted by their patch mass."""
+        """Tree attention pool over the final-normalized tokens x [B, N, d] fp16 -> logits [B, tags] fp32
+        (mlx/haruka.py:104-136): queries compete per token (softmax over the queries) and each token is also gated
+        by sigmoid(logit + bias); 6 coarse queries feed 3 leaf queries each; leaves are weighted by their patch mass.
+
+        Same algebra as the reference with the key/value projection moved onto the queries' side (see __init__):
+        logits = xn @ [Wk_h^T q] + q . bk_h, pooled = (attn^T xn) Wv_h^T + bv_h sum(attn), so the [B, N, 2d] key/value
+        tensor and its per-head transposes are never written; the softmax over queries runs over the contiguous
+        last dimension of [B, N, heads, queries]."""
         cfg = self.cfg
         B, N, d = x.shape
         Hp, C, Q = cfg.pool_heads, cfg.coarse, cfg.leaves
@@ -297,23 +313,30 @@ class HarukaInt8(Int8Engine):
             w, b = self.pool[name]
             return F.layer_norm(t, (d,), w, b, cfg.eps)
 
-        kv = F.linear(ln(x, "norm"), *self.pool_kv)  # [B, N, 2d]; the 1/sqrt(hd) logit scale is in the key rows
-        kt = kv[..., :d].reshape(B, N, Hp, hd).permute(0, 2, 3, 1).contiguous()  # [B, Hp, hd, N]
-        v = kv[..., d:].reshape(B, N, Hp, hd).permute(0, 2, 1, 3).contiguous()  # [B, Hp, N, hd]
+        xn = ln(x, "norm")
 
-        def attend(q, bias):  # q [B, M, d] -> (weights fp32 [B, Hp, M, N], pooled [B, M, d])
-            M = q.shape[1]
-            qh = q.reshape(B, M, Hp, hd).permute(0, 2, 1, 3).contiguous()
-            logits = torch.matmul(qh, kt).float()
-            attn = torch.softmax(logits, dim=2) * torch.sigmoid(logits + bias[:, None])
-            z = torch.matmul(attn.half(), v)
-            return attn, z.permute(0, 2, 1, 3).reshape(B, M, d)
+        def attend(logits, c, bias, M):
+            """logits fp16 [B, N, Hp*M] (column h*M + m) + c -> (mass [B, Hp, M] fp32, pooled [B, M, d] fp16)."""
+            lg = (logits.float() + c.view(-1, 1, Hp * M)).view(B, N, Hp, M)
+            attn = torch.softmax(lg, dim=-1) * torch.sigmoid(lg + bias)
+            mass = attn.sum(1)
+            a_t = torch.empty(B, Hp * M, N, device=x.device, dtype=xn.dtype)
+            a_t.copy_(attn.view(B, N, Hp * M).transpose(1, 2))
+            pooled = torch.bmm(a_t, xn).view(B, Hp, M, d).transpose(0, 1).reshape(Hp, B * M, d)
+            z = torch.bmm(pooled, self.pool_vT).view(Hp, B, M, hd).permute(1, 2, 0, 3).float()
+            z = z + mass.permute(0, 2, 1)[..., None] * self.pool_bv
+            return mass, z.reshape(B, M, d).half()
 
-        _, z = attend(self.q_coarse.expand(B, C, d), self.q_coarse_bias)
+        logits = torch.matmul(xn.view(B * N, d), self.coarse_uT).view(B, N, Hp * C)
+        _, z = attend(logits, self.coarse_c, self.q_coarse_bias, C)
         z_parent = ln(z, "trunk_norm").repeat_interleave(Q // C, dim=1)  # coarse c feeds leaves c*Q/C ..
-        attn, z_child = attend(ln(z_parent + self.q_child, "child_q_norm"), self.q_child_bias)
+        q_leaf = ln(z_parent + self.q_child, "child_q_norm").view(B, Q, Hp, hd)
+        qh = q_leaf.permute(2, 3, 0, 1).reshape(Hp, hd, B * Q)
+        u_t = torch.bmm(self.pool_kT, qh).view(Hp, d, B, Q).permute(2, 1, 0, 3).reshape(B, d, Hp * Q)
+        c_leaf = torch.einsum("he,bqhe->bhq", self.pool_bk, q_leaf.float()).reshape(B, Hp * Q)
+        mass, z_child = attend(torch.bmm(xn, u_t), c_leaf, self.q_child_bias, Q)
         z_tree = ln(z_parent + z_child, "leaf_norm")
-        mass = attn.sum(-1).mean(1)[..., None]  # [B, Q, 1]: patch mass per leaf, averaged over heads
+        mass = mass.mean(1)[..., None]  # [B, Q, 1]: patch mass per leaf, averaged over heads
         z_tree = z_tree * (mass / (mass + 4.0)).half()
         leaf = torch.bmm(z_tree.transpose(0, 1).contiguous(), self.leaf_w).transpose(0, 1) + self.leaf_b
         return F.linear(leaf.reshape(B, Q * cfg.leaf_dim), *self.head).float()
