@@ -33,8 +33,10 @@ SIGNATURES = {
     "ff_gemm_s8": ([_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _int, _int, _vp, _vp, _i64, _f32, _vp], _int),
     "ff_gemm_s8_variants": ([], _int),
     "ff_attention": ([_vp, _vp, _i64, _i64, _i64, _vp], _int),
+    "ff_resample_u8": ([_vp, _i64, _i64, _int, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp],
+                       _int),
 }
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 @cache
@@ -191,6 +193,24 @@ def attention(qkv: torch.Tensor, out: torch.Tensor, seq_len: int) -> None:
     _require(out.shape == (qkv.size(0), C), "out must be [T, C]")
     with torch.cuda.device(qkv.device):
         _check(lib().ff_attention(_ptr(qkv), _ptr(out), qkv.size(0), C // 64, seq_len, _stream(qkv)))
+
+
+def resample_u8(src: torch.Tensor, axis: int, kk: torch.Tensor, bounds: torch.Tensor, row0: int, out: torch.Tensor,
+                region: tuple[int, int, int, int]) -> None:
+    """One Pillow resampling pass (include/foidfinder_rocm.h, ff_resample_u8): src uint8 [H, W, 3] -> out uint8
+    [out_h, out_w, 3], `region` = (top, left, h, w) resampled along axis 0 (width) or 1 (height), the rest white."""
+    _on_gpu(src, kk, bounds, out)
+    _require(src.dtype == out.dtype == torch.uint8 and src.dim() == out.dim() == 3 and src.size(2) == out.size(2) == 3,
+             "src and out must be uint8 [rows, cols, 3]")
+    _require(src.is_contiguous() and out.is_contiguous(), "src and out must be contiguous")
+    _require(kk.dtype == bounds.dtype == torch.int32 and kk.dim() == 2 and bounds.dim() == 2 and bounds.size(1) == 2
+             and kk.is_contiguous() and bounds.is_contiguous(), "kk int32 [n, ksize], bounds int32 [n, 2]")
+    top, left, h, w = region
+    n = w if axis == 0 else h
+    _require(kk.size(0) >= n and bounds.size(0) >= n, "kk/bounds need a row per output index of the region")
+    with torch.cuda.device(src.device):
+        _check(lib().ff_resample_u8(_ptr(src), src.size(0), src.size(1), axis, _ptr(kk), _ptr(bounds), kk.size(1),
+                                    row0, _ptr(out), out.size(0), out.size(1), top, left, h, w, _stream(src)))
 
 
 # ---- torch.ops.foidfinder_rocm registration (schemas as kernels.cu:268-273, plus eps / the fused norm) ----

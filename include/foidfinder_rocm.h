@@ -72,6 +72,18 @@ int ff_gemm_s8_variants(void);
  * seq_len % 96 == 0 there). */
 int ff_attention(const void* qkv, void* out, int64_t T, int64_t heads, int64_t seq_len, void* stream);
 
+/* One pass of Pillow's separable 8-bit resampling (libImaging/Resample.c) over uint8 RGB images [rows, cols, 3].
+ * Output out [out_h, out_w, 3]: inside the region rows top .. top+h-1, columns left .. left+w-1, byte (y, x, c) is
+ * clip((2^21 + sum_t src[...] * kk[o, t]) >> 22, 0, 255) with o = x - left along the width (axis 0: source row
+ * row0 + y - top, columns bounds[o, 0] + t) or o = y - top along the height (axis 1: source rows row0 + bounds[o, 0]
+ * + t, column x - left), t < bounds[o, 1]; every other byte is 255 (white). kk int32 [n, ksize] and bounds int32
+ * [n, 2] with n >= w (axis 0) or n >= h (axis 1); taps whose source index falls outside src are skipped.
+ * Replaces the Haruka letterbox resize pass of the reference's MLX backend, foidfinder/backends/mlx/kernels.py:75-96
+ * (the reference's CUDA backend has no Haruka path). */
+int ff_resample_u8(const uint8_t* src, int64_t src_h, int64_t src_w, int axis, const int32_t* kk,
+                   const int32_t* bounds, int64_t ksize, int64_t row0, uint8_t* out, int64_t out_h, int64_t out_w,
+                   int64_t top, int64_t left, int64_t h, int64_t w, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

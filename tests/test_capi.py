@@ -101,3 +101,22 @@ def test_op_schemas_mirror_the_reference():
     assert "Tensor(a!) out, int epi, int stages, Tensor? rope_cos, Tensor? rope_sin, float q_scale" in schema
     assert "Tensor(a!) out, Tensor(b!) row_scale" in str(ops.rot_q8_1024.default._schema)
     assert "attention(Tensor qkv, Tensor(a!) out, int seq_len)" in str(ops.attention.default._schema)
+
+
+def test_resample_u8_rejects_bad_arguments():
+    lib = K.lib()
+
+    def call(src=(100, 80), axis=0, ksize=5, row0=0, out=(448, 448), region=(0, 0, 100, 40), ptrs=256):
+        top, left, h, w = region
+        return err(lib.ff_resample_u8(ptrs, src[0], src[1], axis, ptrs, ptrs, ksize, row0, ptrs, out[0], out[1], top,
+                                      left, h, w, None))
+
+    assert "axis" in call(axis=2)[1]
+    assert "positive" in call(ksize=0)[1]
+    assert "positive" in call(region=(0, 0, 0, 40))[1]
+    assert "inside the output" in call(region=(400, 0, 100, 40))[1]
+    assert "inside the output" in call(region=(0, -1, 10, 40))[1]
+    assert "outside the source" in call(row0=1)[1]  # axis 0 reads rows row0 .. row0 + h - 1 of 100
+    assert "outside the source" in call(axis=1, region=(0, 0, 10, 81))[1]  # axis 1 reads columns 0 .. w - 1 of 80
+    assert "65535" in call(src=(70000, 3))[1]
+    assert "null" in call(ptrs=None)[1]

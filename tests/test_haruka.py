@@ -215,21 +215,60 @@ def test_model_dir_config_is_recognized(tmp_path):
         load_haruka_dir(tmp_path)
 
 
-def test_haruka_letterbox_is_pillow_bicubic_on_white():
-    """The model card's preprocessing (the reference's tests/test_haruka.py:19-34): white canvas, bicubic resize so
-    the longer side is the input size, centered; transparency composited onto white; raw uint8."""
+RESIZE_CASES = [(850, 1200), (448, 900), (3, 5000), (5000, 3), (100, 37), (448, 300), (1, 1), (1200, 900),
+                (640, 2000), (900, 449), (9, 900), (9, 910), (10, 1001)]
+# the reference's cases (tests/test_haruka.py:36-47), a few more, and both sides of Pillow 12's pass-order boundary
+
+
+def pillow_letterbox(rgb, s=448):
+    """The model card's letterbox by Pillow itself (the reference's tests/test_haruka.py:19-34)."""
     from PIL import Image
 
-    from foidfinder_amd.backends.rocm.preprocess import preprocess_haruka
+    h, w = rgb.shape[:2]
+    if (w, h) == (s, s):
+        return rgb
+    r = min(s / w, s / h)
+    nw, nh = max(1, int(w * r)), max(1, int(h * r))
+    canvas = Image.new("RGB", (s, s), (255, 255, 255))
+    canvas.paste(Image.fromarray(rgb).resize((nw, nh), Image.Resampling.BICUBIC), ((s - nw) // 2, (s - nh) // 2))
+    return np.asarray(canvas)
 
-    rng = np.random.default_rng(8)
-    rgb = rng.integers(0, 256, (90, 40, 3), dtype=np.uint8)  # h 90, w 40 -> 448 x 199, left pad 124
-    out = preprocess_haruka([Image.fromarray(rgb)], 448, device="cpu").numpy()
-    assert out.shape == (1, 448, 448, 3) and out.dtype == np.uint8
-    want = np.asarray(Image.fromarray(rgb).resize((199, 448), Image.Resampling.BICUBIC))
-    assert np.array_equal(out[0, :, 124 : 124 + 199], want)
-    assert (out[0, :, :124] == 255).all() and (out[0, :, 124 + 199 :] == 255).all()
-    same = rng.integers(0, 256, (64, 64, 3), dtype=np.uint8)  # already at the input size: untouched
-    assert np.array_equal(preprocess_haruka([Image.fromarray(same)], 64, device="cpu").numpy()[0], same)
-    rgba = np.zeros((64, 64, 4), np.uint8)  # fully transparent -> white
-    assert (preprocess_haruka([Image.fromarray(rgba, "RGBA")], 64, device="cpu").numpy() == 255).all()
+
+@pytest.mark.parametrize(("w", "h"), RESIZE_CASES)
+def test_oracle_letterbox_is_bit_exact_with_pillow(w, h):
+    from foidfinder_amd.backends.rocm.preprocess import PILLOW_MAJOR
+
+    from oracle import resample as ORS
+
+    rgb = np.random.default_rng(w * h).integers(0, 256, (h, w, 3), dtype=np.uint8)
+    assert np.array_equal(ORS.letterbox(rgb, 448, PILLOW_MAJOR), pillow_letterbox(rgb))
+
+
+def test_pass_order_rules():
+    import importlib
+
+    P = importlib.import_module("foidfinder_amd.backends.rocm.preprocess")  # the module, not the function it exports
+
+    from oracle import resample as ORS
+
+    for w, h in RESIZE_CASES:
+        r = min(448 / w, 448 / h)
+        nw, nh = max(1, int(w * r)), max(1, int(h * r))
+        assert P.vertical_first(w, h, nw, nh) == ORS.vertical_first(w, h, nw, nh, P.PILLOW_MAJOR)
+    # the reference's rule for Pillow 13 (its resize_pad): (448, 900) shrinks the height over twice as much
+    assert ORS.vertical_first(448, 900, 223, 448, 13) and not ORS.vertical_first(850, 1200, 317, 448, 13)
+
+
+def test_bicubic_taps_match_the_oracle():
+    from foidfinder_amd.backends.rocm.preprocess import bicubic_taps
+
+    from oracle import resample as ORS
+
+    for n_in, n_out in ((850, 448), (1200, 448), (3, 1), (5000, 448), (37, 165), (100, 448), (1, 448), (448, 448),
+                        (900, 449), (7, 3)):
+        kk, b = bicubic_taps(n_in, n_out)
+        kk_o, b_o = ORS.coeffs(n_in, n_out)
+        assert np.array_equal(kk, kk_o) and np.array_equal(b, b_o), (n_in, n_out)
+        assert (b[:, 0] >= 0).all() and (b.sum(1) <= n_in).all() and (b[:, 1] <= kk.shape[1]).all()
+        # each row of taps sums to 1 in 22-bit fixed point, within the rounding of its taps
+        assert (np.abs(kk.sum(1).astype(np.int64) - (1 << 22)) <= kk.shape[1]).all()

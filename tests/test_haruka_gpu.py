@@ -211,3 +211,50 @@ def test_rocm_backend_serves_haruka_model_dirs(dev, tmp_path):
     pc = backends.load("rocm", comp).predict(img)
     pt = backends.load("rocm", twin).predict(img)
     assert np.array_equal(pc, pt)
+
+
+RESIZE_CASES = [(850, 1200), (448, 900), (3, 5000), (5000, 3), (100, 37), (448, 300), (1, 1), (1200, 900), (640, 2000),
+                (900, 449), (9, 900), (9, 910), (10, 1001), (448, 448)]
+
+
+@pytest.mark.parametrize(("w", "h"), RESIZE_CASES)
+def test_gpu_letterbox_is_bit_exact_with_pillow(dev, w, h):
+    """The Haruka letterbox on the GPU (ff_resample_u8, two passes) against Pillow's own Image.resize(BICUBIC)
+    pasted on white: the reference's cases (tests/test_haruka.py:36-55), both sides of the installed Pillow's
+    pass-order boundary, and an image already at the input size."""
+    from PIL import Image
+
+    from foidfinder_amd.backends.rocm.preprocess import letterbox_gpu
+
+    s = 448
+    rgb = np.random.default_rng(w * h).integers(0, 256, (h, w, 3), dtype=np.uint8)
+    out = torch.full((s, s, 3), 7, dtype=torch.uint8, device=dev)
+    letterbox_gpu(rgb, s, out)
+    if (w, h) == (s, s):
+        want = rgb
+    else:
+        r = min(s / w, s / h)
+        nw, nh = max(1, int(w * r)), max(1, int(h * r))
+        canvas = Image.new("RGB", (s, s), (255, 255, 255))
+        canvas.paste(Image.fromarray(rgb).resize((nw, nh), Image.Resampling.BICUBIC), ((s - nw) // 2, (s - nh) // 2))
+        want = np.asarray(canvas)
+    assert np.array_equal(out.cpu().numpy(), want)
+
+
+def test_preprocess_haruka_batch(dev):
+    """A batch of mixed images: every slot is its own letterbox; transparency is composited onto white."""
+    from PIL import Image
+
+    from foidfinder_amd.backends.rocm.preprocess import letterbox_gpu, preprocess_haruka
+
+    rng = np.random.default_rng(11)
+    a = Image.fromarray(rng.integers(0, 256, (90, 40, 3), dtype=np.uint8))
+    b = Image.fromarray(np.zeros((64, 64, 4), np.uint8), "RGBA")  # fully transparent -> white
+    c = Image.fromarray(rng.integers(0, 256, (30, 200), dtype=np.uint8), "L").convert("RGB")
+    out = preprocess_haruka([a, b, c], 112, device=dev)
+    assert out.shape == (3, 112, 112, 3) and out.dtype == torch.uint8
+    assert (out[1] == 255).all()
+    for i, im in ((0, a), (2, c)):
+        one = torch.empty(112, 112, 3, dtype=torch.uint8, device=dev)
+        letterbox_gpu(np.asarray(im), 112, one)
+        assert torch.equal(out[i], one)
