@@ -65,13 +65,32 @@ __device__ __forceinline__ float gray_sign(int bit) { return bit ? -1.f : 1.f; }
 // Code of t in [-inf, inf]: clamp to [-127, 127], round half to even, low byte. Adding 1.5 * 2^23 rounds to an
 // integer with ties to even (the ulp there is 1 and 1.5 * 2^23 is even), and the low byte of the sum's bit pattern is
 // the code in two's complement.
-__device__ __forceinline__ uint32_t q8_fast(float t) {
-  const float c = __builtin_amdgcn_fmed3f(t, -127.f, 127.f) + 12582912.f;
-  return __builtin_bit_cast(uint32_t, c) & 0xffu;
+__device__ __forceinline__ uint32_t q8_word(float t) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_fmed3f(t, -127.f, 127.f) + 12582912.f);
 }
 
+// The four codes, a in the low byte: two byte permutes gather the low bytes of (a, b) and (c, d), a third joins them.
 __device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d) {
-  return q8_fast(a) | (q8_fast(b) << 8) | (q8_fast(c) << 16) | (q8_fast(d) << 24);
+  const uint32_t ab = __builtin_amdgcn_perm(q8_word(b), q8_word(a), 0x0c0c0400u);
+  const uint32_t cd = __builtin_amdgcn_perm(q8_word(d), q8_word(c), 0x0c0c0400u);
+  return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
+}
+
+// fp16 inputs folded into their first fp32 operation with v_fma_mix_f32, whose f16 sources convert exactly and whose
+// result rounds once, so each equals the fp32 operation on the converted value: half HI of h2 plus s; and the first
+// butterfly of an (even, odd) column pair held in one register: (lo + hi, lo - hi).
+template <int HI>
+__device__ __forceinline__ float add_h(uint32_t h2, float s) {
+  float r;
+  if constexpr (HI)
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(s));
+  else
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(s));
+  return r;
+}
+__device__ __forceinline__ void bfly0_h(uint32_t h2, float& lo_plus_hi, float& lo_minus_hi) {
+  asm("v_fma_mix_f32 %0, %1, 1.0, %1 op_sel:[0,0,1] op_sel_hi:[1,0,1]" : "=v"(lo_plus_hi) : "v"(h2));
+  asm("v_fma_mix_f32 %0, %1, -1.0, %1 op_sel:[1,0,0] op_sel_hi:[1,0,1]" : "=v"(lo_minus_hi) : "v"(h2));
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -138,20 +157,24 @@ __global__ __launch_bounds__(256) void rot_q8_1024_kernel(const half_t* __restri
   const float s7 = gray_sign(L & 16);
   for (; row < T; row += stride) {
     float v[32];
+    uint32_t w[4][4];  // the row's fp16 pairs (column e in half e & 1 of word e / 2)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[j * 8 + e] = static_cast<float>(nxt[j][e]);
+      for (int k = 0; k < 4; ++k) w[j][k] = __builtin_bit_cast(uint32_t, half2_t{nxt[j][2 * k], nxt[j][2 * k + 1]});
     if (row + stride < T) load(row + stride);
+    auto hv = [&](int i, float s) __attribute__((always_inline)) {  // element i (= 8j + e) + s, one rounding
+      return (i & 1) ? add_h<1>(w[i >> 3][(i & 7) >> 1], s) : add_h<0>(w[i >> 3][(i & 7) >> 1], s);
+    };
     if constexpr (NORM) {
       float s = 0.f;
 #pragma unroll
-      for (int i = 0; i < 32; ++i) s = s + v[i];
+      for (int i = 0; i < 32; ++i) s = hv(i, s);
       const float mean = ref_tree_sum(s) * (1.f / 1024.f);
       float sq = 0.f;
 #pragma unroll
       for (int i = 0; i < 32; ++i) {
-        v[i] = v[i] - mean;
+        v[i] = hv(i, -mean);
         sq = __builtin_fmaf(v[i], v[i], sq);
       }
       const float var = ref_tree_sum(sq) * (1.f / 1024.f);
@@ -167,9 +190,15 @@ __global__ __launch_bounds__(256) void rot_q8_1024_kernel(const half_t* __restri
         }
       }
     }
-    // column bits 0, 1, 2 (registers e)
+    // column bits 0, 1, 2 (registers e); without the norm, bit 0 straight from the fp16 pairs
+    if constexpr (!NORM) {
 #pragma unroll
-    for (int h = 1; h < 8; h <<= 1)
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) bfly0_h(w[j][k], v[j * 8 + 2 * k], v[j * 8 + 2 * k + 1]);
+    }
+#pragma unroll
+    for (int h = NORM ? 1 : 2; h < 8; h <<= 1)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -218,18 +247,22 @@ __global__ __launch_bounds__(256) void rot_q8_1024_kernel(const half_t* __restri
   }
 }
 
-// One row of C = 128*nb columns per 64-lane wave. Lane 16g + l owns, for i = 0..NI-1, the 8 columns
-// (4i + g)*128 + 8*gray(l) + e of block 4i + g: column bits 0-2 in registers, bits 3-6 across the 16 lanes of a DPP
-// row. Stages run over column bits 0..6 in ascending order, as in kernels.cu:125-135. 256-thread workgroups of 4
-// waves stride over the rows, each wave loading its next row while it transforms the current one.
+// One row of C = 128*nb columns per G groups of 16 lanes: G = 4 (a 64-lane wave per row) or G = 2 (a 32-lane
+// half-wave per row, two rows per wave), chosen so that no group idles (h128_groups). Lane 16g + l of a row owns,
+// for i = 0..NI-1, the 8 columns (G i + g)*128 + 8*gray(l) + e of block G i + g: column bits 0-2 in registers, bits
+// 3-6 across the 16 lanes of a DPP row. Stages run over column bits 0..6 in ascending order, as in
+// kernels.cu:125-135. 256-thread workgroups stride over the rows, each wave loading its next rows while it
+// transforms the current ones.
 // LayerNorm (new; EVA02's norm after SwiGLU): gamma/beta are [C] with zeros past c_real, held in LDS (dynamic, 2C
 // floats) for the workgroup's rows; sums over the real columns run per lane sequentially in (i, e) order, then over
-// lanes by the xor tree 32, 16, 15, 7, 3, 1.
-template <int NI, bool NORM>
+// the row's lanes by the xor tree 32 (G = 4 only), 16, 15, 7, 3, 1.
+template <int NI, bool NORM, int G>
 __global__ __launch_bounds__(256) void rot_q8_h128_kernel(const half_t* __restrict__ x, int64_t T, int C, int c_real,
                                                           const float* __restrict__ gamma,
                                                           const float* __restrict__ beta, float eps,
                                                           int8_t* __restrict__ out, float* __restrict__ row_scale) {
+  static_assert(G == 2 || G == 4, "a row spans 2 or 4 groups of 16 lanes");
+  constexpr int RPW = 4 / G;  // rows per wave
   extern __shared__ float4_t gbh[];  // NORM: gamma as C/4 float4, then beta
   const int nb = C >> 7;
   if constexpr (NORM) {
@@ -239,37 +272,48 @@ __global__ __launch_bounds__(256) void rot_q8_h128_kernel(const half_t* __restri
     __syncthreads();
   }
   const int lane = threadIdx.x & 63;
-  const int g = lane >> 4, l16 = lane & 15, gl = l16 ^ (l16 >> 1);
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * 4;
-  int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);  // whole waves share a row
+  const int g = (lane >> 4) & (G - 1), l16 = lane & 15, gl = l16 ^ (l16 >> 1);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 4 * RPW;
+  // whole groups of 16 G lanes share a row; cross-lane operations below stay inside them
+  int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * RPW + (G == 2 ? lane >> 5 : 0);
   half8_t nxt[NI];
   auto load = [&](int64_t r) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const int b = 4 * i + g;
-      if (b < nb) nxt[i] = *reinterpret_cast<const half8_t*>(x + r * C + b * 128 + 8 * gl);
+      const int b = G * i + g;  // lanes of blocks past the row end hold zeros
+      nxt[i] = b < nb ? *reinterpret_cast<const half8_t*>(x + r * C + b * 128 + 8 * gl) : half8_t{};
     }
   };
   if (row < T) load(row);
-  int nreal[NI];  // real columns among the lane's 8 of block 4i + g (a prefix)
+  int nreal[NI];  // real columns among the lane's 8 of block G i + g (a prefix)
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
-    const int b = 4 * i + g;
+    const int b = G * i + g;
     const int left = c_real - (b * 128 + 8 * gl);
     nreal[i] = b < nb ? (left < 0 ? 0 : (left > 8 ? 8 : left)) : 0;
   }
   const float s3 = gray_sign(gl & 1), s4 = gray_sign(gl & 2), s5 = gray_sign(gl & 4), s6 = gray_sign(gl & 8);
+  auto tree_sum = [](float t) __attribute__((always_inline)) {
+    if constexpr (G == 4) t = t + xor_shuffle(t, 32);
+    t = t + swz_xor16(t);
+    t = t + dpp<DPP_XOR15>(t);
+    t = t + dpp<DPP_XOR7>(t);
+    t = t + dpp<DPP_XOR3>(t);
+    return t + dpp<DPP_XOR1>(t);
+  };
   for (; row < T; row += stride) {
     float v[NI * 8];
+    uint32_t w[NI][4];  // the row's fp16 pairs (column e in half e & 1 of word e / 2)
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int b = 4 * i + g;
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[i * 8 + e] = b < nb ? static_cast<float>(nxt[i][e]) : 0.f;
-    }
+      for (int k = 0; k < 4; ++k) w[i][k] = __builtin_bit_cast(uint32_t, half2_t{nxt[i][2 * k], nxt[i][2 * k + 1]});
     if (row + stride < T) load(row + stride);
+    auto hv = [&](int i, int e, float s) __attribute__((always_inline)) {  // column (i, e) + s, one rounding
+      return (e & 1) ? add_h<1>(w[i][e >> 1], s) : add_h<0>(w[i][e >> 1], s);
+    };
     if constexpr (NORM) {
-      // Only block groups past column c_real - 512 can hold padding or the row end (uniform test): the others skip
+      // Only block groups past column c_real - 128 G can hold padding or the row end (uniform test): the others skip
       // the masks. The per-lane counts are re-read opaquely each row so that the compiler cannot hoist 8 * NI
       // loop-invariant lane masks into scalar registers (they would spill).
       int nr[NI];
@@ -281,49 +325,45 @@ __global__ __launch_bounds__(256) void rot_q8_h128_kernel(const half_t* __restri
       float sum = 0.f;
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        if ((4 * i + 4) * 128 > c_real) {
+        if ((G * i + G) * 128 > c_real) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) sum = sum + (e < nr[i] ? v[i * 8 + e] : 0.f);
+          for (int e = 0; e < 8; ++e) {
+            const float t = hv(i, e, sum);  // evaluated on every lane, then selected (no branch around the asm)
+            sum = e < nr[i] ? t : sum;
+          }
         } else {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) sum = sum + v[i * 8 + e];
+          for (int e = 0; e < 8; ++e) sum = hv(i, e, sum);
         }
       }
-      auto tree = [](float t) {
-        t = t + xor_shuffle(t, 32);
-        t = t + swz_xor16(t);
-        t = t + dpp<DPP_XOR15>(t);
-        t = t + dpp<DPP_XOR7>(t);
-        t = t + dpp<DPP_XOR3>(t);
-        return t + dpp<DPP_XOR1>(t);
-      };
       const float fr = static_cast<float>(c_real);
-      const float mean = tree(sum) / fr;
+      const float mean = tree_sum(sum) / fr;
       float sq = 0.f;
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        if ((4 * i + 4) * 128 > c_real) {
+        if ((G * i + G) * 128 > c_real) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const float d = e < nr[i] ? v[i * 8 + e] - mean : 0.f;
+            const float t = hv(i, e, -mean);
+            const float d = e < nr[i] ? t : 0.f;
             v[i * 8 + e] = d;
             sq = __builtin_fmaf(d, d, sq);
           }
         } else {
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const float d = v[i * 8 + e] - mean;
+            const float d = hv(i, e, -mean);
             v[i * 8 + e] = d;
             sq = __builtin_fmaf(d, d, sq);
           }
         }
       }
-      const float var = tree(sq) / fr;
+      const float var = tree_sum(sq) / fr;
       const float rstd = 1.f / sqrtf(var + eps);
       const int n4 = C >> 2;
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        const int b = 4 * i + g;
+        const int b = G * i + g;
         if (b >= nb) continue;  // lanes past the row end keep zeros (they take part in the row's absmax)
         const int c4 = (b * 128 + 8 * gl) >> 2;  // gamma/beta are zero past c_real: no masking inside the row
         const float4_t g0 = gbh[c4], g1 = gbh[c4 + 1], b0 = gbh[n4 + c4], b1 = gbh[n4 + c4 + 1];
@@ -334,9 +374,15 @@ __global__ __launch_bounds__(256) void rot_q8_h128_kernel(const half_t* __restri
         }
       }
     }
-    // column bits 0, 1, 2 (registers)
+    // column bits 0, 1, 2 (registers); without the norm, bit 0 straight from the fp16 pairs
+    if constexpr (!NORM) {
 #pragma unroll
-    for (int h = 1; h < 8; h <<= 1)
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) bfly0_h(w[i][k], v[i * 8 + 2 * k], v[i * 8 + 2 * k + 1]);
+    }
+#pragma unroll
+    for (int h = NORM ? 1 : 2; h < 8; h <<= 1)
 #pragma unroll
       for (int i = 0; i < NI; ++i)
 #pragma unroll
@@ -359,14 +405,17 @@ __global__ __launch_bounds__(256) void rot_q8_h128_kernel(const half_t* __restri
       v[i] = v[i] * 0.08838834764831845f;
       amax = fmaxf(amax, fabsf(v[i]));
     }
-    amax = wave_max(amax);
+    if constexpr (G == 4)
+      amax = wave_max(amax);
+    else
+      amax = half_wave_max(amax);
     const float scale = fmaxf(amax, 1e-12f) / 127.f;
     const float inv = 1.f / scale;
     const float mul = __builtin_popcount(gl) & 1 ? -inv : inv;
     int8_t* orow = out + row * C;
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const int b = 4 * i + g;
+      const int b = G * i + g;
       if (b < nb) {
         uint2 pk;
         pk.x = pack4(v[i * 8] * mul, v[i * 8 + 1] * mul, v[i * 8 + 2] * mul, v[i * 8 + 3] * mul);
@@ -374,7 +423,7 @@ __global__ __launch_bounds__(256) void rot_q8_h128_kernel(const half_t* __restri
         *reinterpret_cast<uint2*>(orow + b * 128 + 8 * gl) = pk;
       }
     }
-    if (lane == 0) row_scale[row] = scale;
+    if ((lane & (16 * G - 1)) == 0) row_scale[row] = scale;
   }
 }
 
@@ -386,16 +435,22 @@ static dim3 stride_grid(const void* kernel, size_t smem, int64_t T, int rows) {
   return dim3(static_cast<unsigned>(std::min<int64_t>((T + rows - 1) / rows, cap)));
 }
 
-template <int NI>
+// 16-lane groups per row: 2 when the block count is even but not a multiple of 4 (768, 2816: no idle group), else 4
+static int h128_groups(int nb) { return nb % 2 == 0 && nb % 4 != 0 && nb / 2 <= 12 ? 2 : 4; }
+
+template <int NI, int G>
 static void launch_h128(hipStream_t st, const half_t* x, int64_t T, int C, int c_real, const float* g, const float* b,
                         float eps, int8_t* out, float* rs) {
+  const int rows_per_block = 4 * (4 / G);
   if (g) {
     const size_t smem = 2 * C * sizeof(float);
-    const dim3 grid = stride_grid(reinterpret_cast<const void*>(&rot_q8_h128_kernel<NI, true>), smem, T, 4);
-    rot_q8_h128_kernel<NI, true><<<grid, 256, smem, st>>>(x, T, C, c_real, g, b, eps, out, rs);
+    const dim3 grid = stride_grid(reinterpret_cast<const void*>(&rot_q8_h128_kernel<NI, true, G>), smem, T,
+                                  rows_per_block);
+    rot_q8_h128_kernel<NI, true, G><<<grid, 256, smem, st>>>(x, T, C, c_real, g, b, eps, out, rs);
   } else {
-    const dim3 grid = stride_grid(reinterpret_cast<const void*>(&rot_q8_h128_kernel<NI, false>), 0, T, 4);
-    rot_q8_h128_kernel<NI, false><<<grid, 256, 0, st>>>(x, T, C, c_real, g, b, eps, out, rs);
+    const dim3 grid = stride_grid(reinterpret_cast<const void*>(&rot_q8_h128_kernel<NI, false, G>), 0, T,
+                                  rows_per_block);
+    rot_q8_h128_kernel<NI, false, G><<<grid, 256, 0, st>>>(x, T, C, c_real, g, b, eps, out, rs);
   }
 }
 
@@ -441,25 +496,28 @@ extern "C" int ff_rot_q8_h128(const void* x, int64_t T, int64_t C, int64_t c_rea
   if (!aligned(x, 16) || !aligned(out, 8) || !aligned(row_scale, 4) || (gamma && (!aligned(gamma, 16) || !aligned(beta, 16))))
     return fail(FF_EINVAL, "rot_q8_h128: misaligned pointer");
   const int nb = static_cast<int>(C / 128);
-  const int ni = (nb + 3) / 4;
+  const int G = h128_groups(nb);
+  const int ni = (nb + G - 1) / G;
   const int cr = gamma ? static_cast<int>(c_real) : static_cast<int>(C);
   const half_t* px = static_cast<const half_t*>(x);
   hipStream_t st = as_stream(stream);
   const int Ci = static_cast<int>(C);
-  switch (ni) {
-    case 1: launch_h128<1>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 2: launch_h128<2>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 3: launch_h128<3>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 4: launch_h128<4>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 5: launch_h128<5>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 6: launch_h128<6>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 7: launch_h128<7>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 8: launch_h128<8>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 9: launch_h128<9>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 10: launch_h128<10>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 11: launch_h128<11>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    case 12: launch_h128<12>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
-    default: return fail(FF_EINVAL, "rot_q8_h128: unsupported C");
+#define FF_H128_CASE(N, GG) \
+  case N: launch_h128<N, GG>(st, px, T, Ci, cr, gamma, beta, eps, out, row_scale); break;
+  if (G == 2) {
+    switch (ni) {
+      FF_H128_CASE(1, 2) FF_H128_CASE(3, 2) FF_H128_CASE(5, 2) FF_H128_CASE(7, 2) FF_H128_CASE(9, 2)
+      FF_H128_CASE(11, 2)
+      default: return fail(FF_EINVAL, "rot_q8_h128: unsupported C");
+    }
+  } else {
+    switch (ni) {
+      FF_H128_CASE(1, 4) FF_H128_CASE(2, 4) FF_H128_CASE(3, 4) FF_H128_CASE(4, 4) FF_H128_CASE(5, 4)
+      FF_H128_CASE(6, 4) FF_H128_CASE(7, 4) FF_H128_CASE(8, 4) FF_H128_CASE(9, 4) FF_H128_CASE(10, 4)
+      FF_H128_CASE(11, 4) FF_H128_CASE(12, 4)
+      default: return fail(FF_EINVAL, "rot_q8_h128: unsupported C");
+    }
   }
+#undef FF_H128_CASE
   return check_launch("rot_q8_h128");
 }

@@ -94,39 +94,48 @@ def rot_q8_1024(
     return quant_rows(v)
 
 
+def h128_groups(C: int) -> int:
+    """16-lane groups per row in the block-128 kernel: 2 (a 32-lane half-wave per row) when the row's block count is
+    even but not a multiple of 4 (768 = 6 blocks, 2816 = 22; at most 12 blocks per group), else 4 (a wave per row)."""
+    nb = C // 128
+    return 2 if nb % 2 == 0 and nb % 4 and nb // 2 <= 12 else 4
+
+
 def layer_norm_h128(v: np.ndarray, c_real: int, gamma: np.ndarray, beta: np.ndarray, eps: float) -> np.ndarray:
     """LayerNorm over the first c_real of C columns (the rest are zero padding and stay zero).
 
-    Reduction order of the HIP kernel that fuses this norm into the block-128 rotation (one 64-lane wave per row):
-    lane 16g + l owns, for i = 0, 1, ..., the columns (4i + g)*128 + 8*gray(l) + e (e = 0..7, gray(l) = l ^ (l >> 1))
-    and sums the real ones sequentially in (i, e) order; the 64 partial sums are combined by the xor tree over lanes
-    32, 16, 15, 7, 3, 1. mean = sum / c_real and var = sumsq / c_real are IEEE divisions; rstd = 1 / sqrt(var + eps).
+    Reduction order of the HIP kernel that fuses this norm into the block-128 rotation (G = h128_groups(C) groups of
+    16 lanes per row): lane 16g + l owns, for i = 0, 1, ..., the columns (G i + g)*128 + 8*gray(l) + e (e = 0..7,
+    gray(l) = l ^ (l >> 1)) and sums the real ones sequentially in (i, e) order; the 16 G partial sums are combined by
+    the xor tree over lanes 32 (G = 4 only), 16, 15, 7, 3, 1. mean = sum / c_real and var = sumsq / c_real are IEEE
+    divisions; rstd = 1 / sqrt(var + eps).
     As in layer_norm_1024, the squares accumulate as fma(d, d, sq) and the output is fma(d * rstd, gamma, beta).
     (The reference has no such fused norm: its CUDA path is PixAI's GELU MLP. The op order follows the EVA02 SwiGLU +
     LayerNorm of foidfinder/backends/mlx/kernels.py:31-72.)"""
     T, C = v.shape
     nb = C // 128
-    ni = (nb + 3) // 4
+    G = h128_groups(C)
+    ni = (nb + G - 1) // G
     real = np.arange(C) < c_real
-    cols = np.full((64, ni * 8), -1, np.int64)  # [lane, i*8 + e] -> column (-1: outside the row)
-    for lane in range(64):
+    cols = np.full((16 * G, ni * 8), -1, np.int64)  # [lane, i*8 + e] -> column (-1: outside the row)
+    for lane in range(16 * G):
         g, l16 = lane >> 4, lane & 15
         gl = l16 ^ (l16 >> 1)
         for i in range(ni):
-            b = 4 * i + g
+            b = G * i + g
             if b < nb:
                 cols[lane, i * 8 : i * 8 + 8] = b * 128 + 8 * gl + np.arange(8)
     valid = (cols >= 0) & real[np.maximum(cols, 0)]
     safe = np.maximum(cols, 0)
     gathered = np.where(valid[None], v[:, safe], F32(0.0))  # [T, 64, ni*8]
-    s = np.zeros((T, 64), F32)
+    s = np.zeros((T, 16 * G), F32)
     for k in range(ni * 8):
         s = s + gathered[:, :, k]
-    masks = (32, 16, 15, 7, 3, 1)
+    masks = (32, 16, 15, 7, 3, 1) if G == 4 else (16, 15, 7, 3, 1)
     mean = _xor_tree(s, masks) / F32(c_real)
     d = np.where(real[None, :], v - mean[:, None], F32(0.0)).astype(F32)
     dg = np.where(valid[None], d[:, safe], F32(0.0))
-    sq = np.zeros((T, 64), F32)
+    sq = np.zeros((T, 16 * G), F32)
     for k in range(ni * 8):
         sq = fma32(dg[:, :, k], dg[:, :, k], sq)
     var = _xor_tree(sq, masks) / F32(c_real)
