@@ -18,7 +18,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 INCLUDE = PKG.parent / "include"
 LIB = PKG / "libfoidfinder_rocm.so"
-SOURCES = ["capi.hip", "rotq8.hip", "gemm_s8.hip", "attention.hip", "resample.hip"]
+SOURCES = ["capi.hip", "rotq8.hip", "gemm_s8.hip", "attention.hip", "resample.hip", "pool.hip"]
 ARCH = "gfx950"
 
 FLAGS = [

@@ -52,6 +52,6 @@ int64_t resident_blocks(const void* kernel, int block, size_t smem) {
 
 }  // namespace ff
 
-extern "C" int ff_abi_version(void) { return 2; }
+extern "C" int ff_abi_version(void) { return 3; }
 
 extern "C" const char* ff_last_error(void) { return ff::g_error.c_str(); }

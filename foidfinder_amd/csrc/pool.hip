@@ -1,0 +1,164 @@
+// The memory-bound steps of Haruka's slot-sigmoid tree pool (foidfinder/backends/mlx/haruka.py:104-136) on gfx950:
+//
+//  * layer_norm2: the backbone's final LayerNorm, rounded to fp16, then the pool's own LayerNorm, in one pass over
+//    the tokens (the reference applies them one after the other, each returning fp16).
+//  * slot_weights: per token and pool head, the weights of M competing queries, softmax over the queries times
+//    sigmoid(logit + bias), written transposed (query-major rows over the tokens, the layout of the pooling product)
+//    with per-block sums over the tokens (each query's mass).
+#include "common.h"
+
+namespace ff {
+
+// One wave per row of C (C % 64 == 0, C <= 2048): lane l holds columns l + 64 k. Means and variances are two-pass
+// (sum, then squared deviations) in fp32, rstd = 1 / sqrt(var + eps).
+template <int PER>
+__global__ __launch_bounds__(256) void layer_norm2_kernel(const half_t* __restrict__ x, int64_t T, int C,
+                                                          const half_t* __restrict__ g1, const half_t* __restrict__ b1,
+                                                          const half_t* __restrict__ g2, const half_t* __restrict__ b2,
+                                                          float eps, half_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= T) return;
+  const half_t* xr = x + row * C;
+  float v[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) v[k] = 64 * k + lane < C ? static_cast<float>(xr[64 * k + lane]) : 0.f;
+  const float inv_c = 1.f / static_cast<float>(C);
+  auto norm = [&](const half_t* g, const half_t* b, bool round_fp16) __attribute__((always_inline)) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) s += v[k];
+#pragma unroll
+    for (int m = 32; m; m >>= 1) s += xor_shuffle(s, m);
+    const float mean = s * inv_c;
+    float q = 0.f;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const float d = 64 * k + lane < C ? v[k] - mean : 0.f;
+      q += d * d;
+    }
+#pragma unroll
+    for (int m = 32; m; m >>= 1) q += xor_shuffle(q, m);
+    const float rstd = 1.f / sqrtf(q * inv_c + eps);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int c = 64 * k + lane;
+      if (c < C) {
+        const float y = (v[k] - mean) * rstd * static_cast<float>(g[c]) + static_cast<float>(b[c]);
+        v[k] = round_fp16 ? static_cast<float>(static_cast<half_t>(y)) : y;
+      }
+    }
+  };
+  norm(g1, b1, true);
+  norm(g2, b2, false);
+  half_t* orow = out + row * C;
+#pragma unroll
+  for (int k = 0; k < PER; ++k)
+    if (64 * k + lane < C) orow[64 * k + lane] = static_cast<half_t>(v[k]);
+}
+
+// Tokens per workgroup of slot_weights.
+constexpr int SW_TOKENS = 32;
+
+// Grid (token blocks of 32, batch). Thread t handles pairs (token, head) p = t, t + 256, ... of the block's 32 x G:
+// it reads the pair's M logits (+ c, the queries' key-bias terms), computes the weights in fp32 and puts them into an
+// LDS tile [G*M][32] (transposed); the tile is then written out row by row (32 contiguous tokens per query column,
+// two columns per wave), and each column's fp32 sum over the block's tokens goes to partial[b, block, column].
+template <int M>
+__global__ __launch_bounds__(256) void slot_weights_kernel(const half_t* __restrict__ logits, const float* __restrict__ c,
+                                                           int64_t c_stride, const float* __restrict__ bias, int N,
+                                                           int G, half_t* __restrict__ a_t,
+                                                           float* __restrict__ partial) {
+  extern __shared__ float tile[];  // [G*M][SW_TOKENS + 1] fp32 weights
+  const int GM = G * M, b = blockIdx.y, n0 = blockIdx.x * SW_TOKENS;
+  const int ntok = min(SW_TOKENS, N - n0);
+  const half_t* lg = logits + (static_cast<int64_t>(b) * N + n0) * GM;
+  const float* cb = c + b * c_stride;
+  float bi[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) bi[m] = bias[m];
+  for (int p = threadIdx.x; p < SW_TOKENS * G; p += 256) {
+    const int t = p / G, h = p % G;
+    float l[M];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      l[m] = t < ntok ? static_cast<float>(lg[static_cast<int64_t>(t) * GM + h * M + m]) + cb[h * M + m] : 0.f;
+      mx = fmaxf(mx, l[m]);
+    }
+    float e[M], s = 0.f;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      e[m] = __expf(l[m] - mx);
+      s += e[m];
+    }
+    const float inv = 1.f / s;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float gate = 1.f / (1.f + __expf(-(l[m] + bi[m])));
+      tile[(h * M + m) * (SW_TOKENS + 1) + t] = t < ntok ? e[m] * inv * gate : 0.f;
+    }
+  }
+  __syncthreads();
+  // rows of the transposed tile: each half-wave takes one query column at a time, a lane per token
+  const int half = threadIdx.x >> 5, lane = threadIdx.x & 31;
+  for (int j = half; j < GM; j += 8) {
+    const float w = tile[j * (SW_TOKENS + 1) + lane];
+    if (lane < ntok) a_t[(static_cast<int64_t>(b) * GM + j) * N + n0 + lane] = static_cast<half_t>(w);
+    float s = w;
+#pragma unroll
+    for (int m = 16; m; m >>= 1) s += xor_shuffle(s, m);
+    if (lane == 0) partial[(static_cast<int64_t>(b) * gridDim.x + blockIdx.x) * GM + j] = s;
+  }
+}
+
+}  // namespace ff
+
+using namespace ff;
+
+extern "C" int ff_layer_norm2(const void* x, int64_t T, int64_t C, const void* g1, const void* b1, const void* g2,
+                              const void* b2, float eps, void* out, void* stream) {
+  clear_error();
+  if (T < 0 || C <= 0 || C % 64 != 0 || C > 2048)
+    return fail(FF_EINVAL, "layer_norm2: need T >= 0 and 0 < C <= 2048, C % 64 == 0");
+  if (!(eps > 0.f)) return fail(FF_EINVAL, "layer_norm2: eps must be > 0");
+  if (T == 0) return FF_OK;
+  if (!x || !g1 || !b1 || !g2 || !b2 || !out) return fail(FF_EINVAL, "layer_norm2: null pointer");
+  const dim3 grid(static_cast<unsigned>((T + 3) / 4));
+  const hipStream_t st = as_stream(stream);
+  const auto* px = static_cast<const half_t*>(x);
+  const auto *pg1 = static_cast<const half_t*>(g1), *pb1 = static_cast<const half_t*>(b1);
+  const auto *pg2 = static_cast<const half_t*>(g2), *pb2 = static_cast<const half_t*>(b2);
+  auto* po = static_cast<half_t*>(out);
+  const int Ci = static_cast<int>(C);
+  if (C <= 768)
+    layer_norm2_kernel<12><<<grid, 256, 0, st>>>(px, T, Ci, pg1, pb1, pg2, pb2, eps, po);
+  else
+    layer_norm2_kernel<32><<<grid, 256, 0, st>>>(px, T, Ci, pg1, pb1, pg2, pb2, eps, po);
+  return check_launch("layer_norm2");
+}
+
+extern "C" int64_t ff_slot_weights_blocks(int64_t N) { return N > 0 ? (N + SW_TOKENS - 1) / SW_TOKENS : 0; }
+
+extern "C" int ff_slot_weights(const void* logits, const float* c, int64_t c_stride, const float* bias, int64_t B,
+                               int64_t N, int64_t G, int64_t M, void* a_t, float* partial, void* stream) {
+  clear_error();
+  if (B < 0 || N <= 0 || N > 0x7fffffff || G <= 0 || G > 64) return fail(FF_EINVAL, "slot_weights: bad B, N or G");
+  if (M != 6 && M != 18) return fail(FF_EINVAL, "slot_weights: M must be 6 or 18 (the tree pool's query counts)");
+  if (B > 65535) return fail(FF_EINVAL, "slot_weights: B > 65535");
+  if (c_stride != 0 && c_stride < G * M) return fail(FF_EINVAL, "slot_weights: c_stride must be 0 or >= G*M");
+  if (B == 0) return FF_OK;
+  if (!logits || !c || !bias || !a_t || !partial) return fail(FF_EINVAL, "slot_weights: null pointer");
+  const size_t smem = static_cast<size_t>(G * M) * (SW_TOKENS + 1) * sizeof(float);
+  if (smem > 64 * 1024) return fail(FF_EINVAL, "slot_weights: G*M too large (LDS tile above 64 KB)");
+  const dim3 grid(static_cast<unsigned>(ff_slot_weights_blocks(N)), static_cast<unsigned>(B));
+  const hipStream_t st = as_stream(stream);
+  const auto* pl = static_cast<const half_t*>(logits);
+  auto* pa = static_cast<half_t*>(a_t);
+  const int Ni = static_cast<int>(N), Gi = static_cast<int>(G);
+  if (M == 6)
+    slot_weights_kernel<6><<<grid, 256, smem, st>>>(pl, c, c_stride, bias, Ni, Gi, pa, partial);
+  else
+    slot_weights_kernel<18><<<grid, 256, smem, st>>>(pl, c, c_stride, bias, Ni, Gi, pa, partial);
+  return check_launch("slot_weights");
+}

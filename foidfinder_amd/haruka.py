@@ -31,7 +31,7 @@ import torch
 import torch.nn.functional as F
 
 from .engine import Int8Engine, eva02_rope_tables, rotate_quantize
-from .kernels import EPI_QKV_ROPE, EPI_RESIDUAL, EPI_SWIGLU, kernels, pad_norm
+from .kernels import EPI_QKV_ROPE, EPI_RESIDUAL, EPI_SWIGLU, kernels, pad_norm, slot_weights_blocks
 
 ARCHITECTURE = "haruka-eva02-tree"  # foidfinder/haruka.py:14
 QUANTIZED = ("qkv", "proj", "fc1", "fc2")  # the backbone linears that run as W8A8
@@ -296,15 +296,16 @@ class HarukaInt8(Int8Engine):
         return x.reshape(B * g * g, p * p * 3)
 
     def pool_head(self, x: torch.Tensor) -> torch.Tensor:
-        """Tree attention pool over the final-normalized tokens x [B, N, d] fp16 -> logits [B, tags] fp32
-        (mlx/haruka.py:104-136): queries compete per token (softmax over the queries) and each token is also gated
+        """Final LayerNorm + tree attention pool over the residual stream x [B, N, d] fp16 -> logits [B, tags] fp32
+        (mlx/haruka.py:100-136): queries compete per token (softmax over the queries) and each token is also gated
         by sigmoid(logit + bias); 6 coarse queries feed 3 leaf queries each; leaves are weighted by their patch mass.
 
         Same algebra as the reference with the key/value projection moved onto the queries' side (see __init__):
-        logits = xn @ [Wk_h^T q] + q . bk_h, pooled = (attn^T xn) Wv_h^T + bv_h sum(attn), so the [B, N, 2d] key/value
-        tensor and its per-head transposes are never written; the softmax over queries runs over the contiguous
-        last dimension of [B, N, heads, queries]."""
-        cfg = self.cfg
+        logits = xn @ [Wk_h^T q] + q . bk_h, pooled = (w^T xn) Wv_h^T + bv_h sum(w), so the [B, N, 2d] key/value
+        tensor is never formed. The two LayerNorms (backbone, then pool) are one kernel (ff_layer_norm2), and the
+        weights w (softmax over queries x sigmoid gate), their transpose for the pooling product and their sums over
+        the tokens are another (ff_slot_weights)."""
+        cfg, k = self.cfg, self.k
         B, N, d = x.shape
         Hp, C, Q = cfg.pool_heads, cfg.coarse, cfg.leaves
         hd = d // Hp
@@ -313,15 +314,16 @@ class HarukaInt8(Int8Engine):
             w, b = self.pool[name]
             return F.layer_norm(t, (d,), w, b, cfg.eps)
 
-        xn = ln(x, "norm")
+        xn = torch.empty_like(x)
+        k.layer_norm2(x, *self.norm, *self.pool["norm"], cfg.eps, xn)
+        nblk = slot_weights_blocks(N)
 
         def attend(logits, c, bias, M):
             """logits fp16 [B, N, Hp*M] (column h*M + m) + c -> (mass [B, Hp, M] fp32, pooled [B, M, d] fp16)."""
-            lg = (logits.float() + c.view(-1, 1, Hp * M)).view(B, N, Hp, M)
-            attn = torch.softmax(lg, dim=-1) * torch.sigmoid(lg + bias)
-            mass = attn.sum(1)
-            a_t = torch.empty(B, Hp * M, N, device=x.device, dtype=xn.dtype)
-            a_t.copy_(attn.view(B, N, Hp * M).transpose(1, 2))
+            a_t = torch.empty(B, Hp * M, N, device=x.device, dtype=torch.half)
+            partial = torch.empty(B, nblk, Hp * M, device=x.device, dtype=torch.float32)
+            k.slot_weights(logits, c, bias, Hp, a_t, partial)
+            mass = partial.sum(1).view(B, Hp, M)
             pooled = torch.bmm(a_t, xn).view(B, Hp, M, d).transpose(0, 1).reshape(Hp, B * M, d)
             z = torch.bmm(pooled, self.pool_vT).view(Hp, B, M, hd).permute(1, 2, 0, 3).float()
             z = z + mass.permute(0, 2, 1)[..., None] * self.pool_bv
@@ -333,7 +335,7 @@ class HarukaInt8(Int8Engine):
         q_leaf = ln(z_parent + self.q_child, "child_q_norm").view(B, Q, Hp, hd)
         qh = q_leaf.permute(2, 3, 0, 1).reshape(Hp, hd, B * Q)
         u_t = torch.bmm(self.pool_kT, qh).view(Hp, d, B, Q).permute(2, 1, 0, 3).reshape(B, d, Hp * Q)
-        c_leaf = torch.einsum("he,bqhe->bhq", self.pool_bk, q_leaf.float()).reshape(B, Hp * Q)
+        c_leaf = torch.einsum("he,bqhe->bhq", self.pool_bk, q_leaf.float()).reshape(B, Hp * Q).contiguous()
         mass, z_child = attend(torch.bmm(xn, u_t), c_leaf, self.q_child_bias, Q)
         z_tree = ln(z_parent + z_child, "leaf_norm")
         mass = mass.mean(1)[..., None]  # [B, Q, 1]: patch mass per leaf, averaged over heads
@@ -371,7 +373,7 @@ class HarukaInt8(Int8Engine):
             self._gemm(buf["h8"], lw["fc2"], rs, EPI_RESIDUAL, v["fc2"], x)
             if trace is not None:
                 trace[f"x{i}"] = x.clone()
-        return self.pool_head(F.layer_norm(xv, (d,), *self.norm, eps))
+        return self.pool_head(xv)
 
 
 def load_haruka_dir(model_dir: str | Path, device: str | torch.device = "cuda", **overrides) -> tuple[HarukaInt8, dict]:

@@ -35,8 +35,11 @@ SIGNATURES = {
     "ff_attention": ([_vp, _vp, _i64, _i64, _i64, _vp], _int),
     "ff_resample_u8": ([_vp, _i64, _i64, _int, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp],
                        _int),
+    "ff_layer_norm2": ([_vp, _i64, _i64, _vp, _vp, _vp, _vp, _f32, _vp, _vp], _int),
+    "ff_slot_weights_blocks": ([_i64], _i64),
+    "ff_slot_weights": ([_vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp], _int),
 }
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 @cache
@@ -213,6 +216,41 @@ def resample_u8(src: torch.Tensor, axis: int, kk: torch.Tensor, bounds: torch.Te
                                     row0, _ptr(out), out.size(0), out.size(1), top, left, h, w, _stream(src)))
 
 
+def layer_norm2(x: torch.Tensor, g1: torch.Tensor, b1: torch.Tensor, g2: torch.Tensor, b2: torch.Tensor, eps: float,
+                out: torch.Tensor) -> None:
+    """out = LN(fp16(LN(x; g1, b1)); g2, b2) over the last dimension of fp16 x [..., C] (fp16 params [C])."""
+    _on_gpu(x, g1, b1, g2, b2, out)
+    C = x.size(-1)
+    _require(x.dtype == out.dtype == torch.float16 and x.is_contiguous() and out.is_contiguous()
+             and out.shape == x.shape, "x and out must be contiguous fp16 of one shape")
+    _require(all(t.dtype == torch.float16 and t.numel() == C for t in (g1, b1, g2, b2)), "params must be fp16 [C]")
+    with torch.cuda.device(x.device):
+        _check(lib().ff_layer_norm2(_ptr(x), x.numel() // C, C, _ptr(g1), _ptr(b1), _ptr(g2), _ptr(b2), eps, _ptr(out),
+                                    _stream(x)))
+
+
+def slot_weights_blocks(N: int) -> int:
+    return lib().ff_slot_weights_blocks(N)
+
+
+def slot_weights(logits: torch.Tensor, c: torch.Tensor, bias: torch.Tensor, heads: int, a_t: torch.Tensor,
+                 partial: torch.Tensor) -> None:
+    """Tree-pool weights (include/foidfinder_rocm.h, ff_slot_weights): logits fp16 [B, N, heads*M] + c fp32 ([heads*M]
+    shared or [B, heads*M]) -> a_t fp16 [B, heads*M, N], partial fp32 [B, blocks, heads*M]."""
+    _on_gpu(logits, c, bias, a_t, partial)
+    B, N, GM = logits.shape
+    M = bias.numel()
+    _require(logits.dtype == torch.float16 and logits.is_contiguous() and GM == heads * M, "logits fp16 [B, N, heads*M]")
+    _require(c.dtype == bias.dtype == torch.float32 and c.is_contiguous() and bias.is_contiguous(), "c, bias fp32")
+    _require(c.numel() in (GM, B * GM), "c must be [heads*M] or [B, heads*M]")
+    _require(a_t.dtype == torch.float16 and a_t.is_contiguous() and a_t.shape == (B, GM, N), "a_t fp16 [B, heads*M, N]")
+    _require(partial.dtype == torch.float32 and partial.is_contiguous()
+             and partial.shape == (B, slot_weights_blocks(N), GM), "partial fp32 [B, blocks, heads*M]")
+    with torch.cuda.device(logits.device):
+        _check(lib().ff_slot_weights(_ptr(logits), _ptr(c), 0 if c.numel() == GM else GM, _ptr(bias), B, N, heads, M,
+                                     _ptr(a_t), _ptr(partial), _stream(logits)))
+
+
 # ---- torch.ops.foidfinder_rocm registration (schemas as kernels.cu:268-273, plus eps / the fused norm) ----
 
 _LIB = torch.library.Library("foidfinder_rocm", "DEF")
@@ -229,6 +267,11 @@ _LIB.impl("gemm_s8", gemm_s8, "CUDA")
 _LIB.impl("rot_q8_1024", rot_q8_1024, "CUDA")
 _LIB.impl("rot_q8_h128", rot_q8_h128, "CUDA")
 _LIB.impl("attention", attention, "CUDA")
+# Haruka's tree pool (no reference CUDA op; out-param ops in the same style)
+_LIB.define("layer_norm2(Tensor x, Tensor g1, Tensor b1, Tensor g2, Tensor b2, float eps, Tensor(a!) out) -> ()")
+_LIB.define("slot_weights(Tensor logits, Tensor c, Tensor bias, int heads, Tensor(a!) a_t, Tensor(b!) partial) -> ()")
+_LIB.impl("layer_norm2", layer_norm2, "CUDA")
+_LIB.impl("slot_weights", slot_weights, "CUDA")
 
 
 @cache

@@ -120,3 +120,21 @@ def test_resample_u8_rejects_bad_arguments():
     assert "outside the source" in call(axis=1, region=(0, 0, 10, 81))[1]  # axis 1 reads columns 0 .. w - 1 of 80
     assert "65535" in call(src=(70000, 3))[1]
     assert "null" in call(ptrs=None)[1]
+
+
+def test_pool_kernels_reject_bad_arguments():
+    lib = K.lib()
+    assert "C <= 2048" in err(lib.ff_layer_norm2(256, 4, 100, 256, 256, 256, 256, 1e-6, 256, None))[1]
+    assert "eps" in err(lib.ff_layer_norm2(256, 4, 768, 256, 256, 256, 256, 0.0, 256, None))[1]
+    assert lib.ff_layer_norm2(None, 0, 768, None, None, None, None, 1e-6, None, None) == FF_OK
+    assert lib.ff_slot_weights_blocks(1025) == 33 and lib.ff_slot_weights_blocks(0) == 0
+
+    def sw(B=2, N=1025, G=16, M=18, c_stride=0, ptrs=256):
+        return err(lib.ff_slot_weights(ptrs, ptrs, c_stride, ptrs, B, N, G, M, ptrs, ptrs, None))
+
+    assert "M must be 6 or 18" in sw(M=7)[1]
+    assert "bad B, N or G" in sw(N=0)[1]
+    assert "c_stride" in sw(c_stride=5)[1]
+    assert "LDS" in sw(G=64)[1]
+    assert "null" in sw(ptrs=None)[1]
+    assert sw(B=0) == (FF_OK, "")

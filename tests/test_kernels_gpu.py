@@ -304,3 +304,48 @@ def test_attention_identical_keys_give_mean_of_values(dev, rng):
     got = run_attention(dev, qkv, L).astype(np.float64)
     v = qkv[:, 2 * H * 64 :].astype(np.float64)
     np.testing.assert_allclose(got, np.broadcast_to(v.mean(0), got.shape), atol=2e-3)
+
+
+def test_layer_norm2_matches_two_float_layer_norms(dev, rng):
+    """ff_layer_norm2 against two float64 LayerNorms with the fp16 rounding between them (768 and 2048 columns)."""
+    from foidfinder_amd import kernels as K
+
+    for T, C in ((300, 768), (5, 2048), (1, 64)):
+        x = (rng.standard_normal((T, C)) * 3 + 0.5).astype(np.float16)
+        g1, b1, g2, b2 = ((1 + 0.1 * rng.standard_normal(C)).astype(np.float16), (0.1 * rng.standard_normal(C)).astype(np.float16),
+                          (1 + 0.1 * rng.standard_normal(C)).astype(np.float16), (0.1 * rng.standard_normal(C)).astype(np.float16))
+        out = torch.empty(T, C, dtype=torch.float16, device=dev)
+        K.layer_norm2(*(to_gpu(a, dev) for a in (x, g1, b1, g2, b2)), 1e-6, out)
+        torch.cuda.synchronize()
+
+        def ln(v, g, b):
+            v = v.astype(np.float64)
+            m = v.mean(-1, keepdims=True)
+            return (v - m) / np.sqrt(((v - m) ** 2).mean(-1, keepdims=True) + 1e-6) * g.astype(np.float64) + b.astype(np.float64)
+
+        want = ln(ln(x, g1, b1).astype(np.float16), g2, b2)
+        assert np.abs(out.cpu().numpy().astype(np.float64) - want).max() < 8e-3 * max(1.0, np.abs(want).max())
+
+
+@pytest.mark.parametrize(("B", "N", "G", "M", "shared_c"), [(2, 1025, 16, 6, True), (3, 65, 16, 18, False),
+                                                             (1, 31, 4, 18, False), (2, 96, 16, 18, True)])
+def test_slot_weights_matches_float(dev, rng, B, N, G, M, shared_c):
+    """ff_slot_weights: softmax over the M queries times sigmoid(logit + bias), transposed, and the per-block sums
+    over the tokens (summed over blocks: each query's mass), against float64."""
+    from foidfinder_amd import kernels as K
+
+    logits = (rng.standard_normal((B, N, G * M)) * 3).astype(np.float16)
+    c = (rng.standard_normal(G * M if shared_c else (B, G * M)) * 0.5).astype(np.float32)
+    bias = (-2 + 0.3 * rng.standard_normal(M)).astype(np.float32)
+    nblk = K.slot_weights_blocks(N)
+    a_t = torch.full((B, G * M, N), 7.0, dtype=torch.float16, device=dev)
+    partial = torch.empty(B, nblk, G * M, dtype=torch.float32, device=dev)
+    K.slot_weights(to_gpu(logits, dev), to_gpu(c, dev), to_gpu(bias, dev), G, a_t, partial)
+    torch.cuda.synchronize()
+    l = logits.astype(np.float64).reshape(B, N, G, M) + c.astype(np.float64).reshape(-1, 1, G, M)
+    e = np.exp(l - l.max(-1, keepdims=True))
+    w = e / e.sum(-1, keepdims=True) / (1 + np.exp(-(l + bias.astype(np.float64))))
+    want = w.reshape(B, N, G * M).transpose(0, 2, 1)
+    assert np.abs(a_t.cpu().numpy().astype(np.float64) - want).max() < 1e-3
+    mass = partial.sum(1).cpu().numpy().astype(np.float64)
+    assert np.abs(mass - want.sum(-1)).max() < 1e-4 * N
