@@ -1,4 +1,4 @@
-// The memory-bound steps of Haruka's slot-sigmoid tree pool (foidfinder/backends/mlx/haruka.py:104-136) on gfx950:
+// The memory-bound steps of Haruka's slot-sigmoid tree pool (foidfinder/backends/mlx/haruka.py:101-133) on gfx950:
 //
 //  * layer_norm2: the backbone's final LayerNorm, rounded to fp16, then the pool's own LayerNorm, in one pass over
 //    the tokens (the reference applies them one after the other, each returning fp16).

@@ -86,15 +86,15 @@ int ff_resample_u8(const uint8_t* src, int64_t src_h, int64_t src_w, int axis, c
 
 /* Two LayerNorms in a row over fp16 rows of C (C % 64 == 0, C <= 2048): y = LN(x; g1, b1) rounded to fp16, then
  * out = LN(y; g2, b2) in fp16; fp16 gamma/beta [C], epsilon eps for both. Haruka's final backbone norm followed by its
- * pool's norm (foidfinder/backends/mlx/haruka.py:100, :117); no counterpart in the reference's CUDA backend. */
+ * pool's norm (foidfinder/backends/mlx/haruka.py:101, :122); no counterpart in the reference's CUDA backend. */
 int ff_layer_norm2(const void* x, int64_t T, int64_t C, const void* g1, const void* b1, const void* g2,
                    const void* b2, float eps, void* out, void* stream);
 
 /* Token blocks of ff_slot_weights for N tokens (the second dimension of its `partial` output). */
 int64_t ff_slot_weights_blocks(int64_t N);
 
-/* Slot-sigmoid pooling weights of Haruka's tree pool (foidfinder/backends/mlx/haruka.py:112-115): per batch b,
- * token n and pool head h, with l[m] = logits[b, n, h*M + m] + c[b*c_stride + h*M + m] (c_stride 0: c shared by the
+/* Slot-sigmoid pooling weights of Haruka's tree pool (foidfinder/backends/mlx/haruka.py:116-119, masses :133):
+ * per batch b, token n and pool head h, with l[m] = logits[b, n, h*M + m] + c[b*c_stride + h*M + m] (c_stride 0: c shared by the
  * batch), w[m] = softmax_m(l)[m] * sigmoid(l[m] + bias[m]) over the M queries (M = 6 or 18). Writes a_t fp16
  * [B, G*M, N] (a_t[b, h*M + m, n] = w[m], query-major rows over the tokens) and partial fp32
  * [B, ff_slot_weights_blocks(N), G*M] (each row the sums of w over one block of tokens; summing over the blocks

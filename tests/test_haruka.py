@@ -272,3 +272,24 @@ def test_bicubic_taps_match_the_oracle():
         assert (b[:, 0] >= 0).all() and (b.sum(1) <= n_in).all() and (b[:, 1] <= kk.shape[1]).all()
         # each row of taps sums to 1 in 22-bit fixed point, within the rounding of its taps
         assert (np.abs(kk.sum(1).astype(np.int64) - (1 << 22)) <= kk.shape[1]).all()
+
+
+def test_bicubic_taps_match_the_pillow_known_answers():
+    """The reference's own Pillow tap tables (web/src/engine/engine.test.ts:8-34), kept as a fixture."""
+    from pathlib import Path
+
+    from foidfinder_amd.backends.rocm.preprocess import bicubic_taps
+
+    from oracle import resample as ORS
+
+    cases = json.loads((Path(__file__).parent / "golden" / "pillow_bicubic_taps.json").read_text())["cases"]
+    assert len(cases) == 5
+    for key, want in cases.items():
+        n_in, n_out = map(int, key.split("->"))
+        for kk, b in (bicubic_taps(n_in, n_out), ORS.coeffs(n_in, n_out)):
+            flat = kk.astype(np.int64).ravel()
+            assert kk.shape[1] == want["ksize"], key
+            assert kk[0].tolist() == want["row0"], key
+            assert int((flat * np.arange(1, flat.size + 1)).sum()) == want["checksum"], key
+            assert int(b.astype(np.int64).sum()) == want["boundsSum"], key
+            assert b[0].tolist() == want["first"] and b[-1].tolist() == want["last"], key
