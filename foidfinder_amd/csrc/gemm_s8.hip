@@ -858,13 +858,8 @@ __global__ __launch_bounds__(512, 1) void gemm_s8_persist_kernel(const GemmArgs 
     }
   };
 
+  // No zero fill: a tile's first k-step writes the accumulators from an inline-constant zero C operand.
   int16_t_v acc[NI][MI];
-#pragma unroll
-  for (int i = 0; i < NI; ++i)
-#pragma unroll
-    for (int j = 0; j < MI; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
   const int fr = lane & 31, fk = lane >> 5;
   int4_t xw[2][NI], ya[2][MI];
@@ -884,14 +879,15 @@ __global__ __launch_bounds__(512, 1) void gemm_s8_persist_kernel(const GemmArgs 
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   read_frags(0, 0, 0);
-  int kt = 0, r = 0, m0, n0;
+  int r = 0, m0, n0;
   coords(0, m0, n0);
   // Slice g: slice g + 1 is issued into the other slot (free: every wave passed the barrier after reading it);
   // the k-steps run in order, each while the next one's fragments are read; before the last one, slice g + 1 is
   // waited for (and the barrier passed), so its first fragments are read while slice g's last k-step computes.
   // After a tile's last slice they are read once more after the epilogue; after the final slice the reads hit a
-  // stale slot and are never used.
-  auto slice = [&](int g) __attribute__((always_inline)) {
+  // stale slot and are never used. FIRST: the tile's first slice, whose first k-step starts from C = 0.
+  auto slice = [&](int g, auto first_c) __attribute__((always_inline)) {
+    constexpr bool FIRST = decltype(first_c)::value;
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk) {
       const int b = kk & 1;
@@ -902,11 +898,13 @@ __global__ __launch_bounds__(512, 1) void gemm_s8_persist_kernel(const GemmArgs 
         __builtin_amdgcn_s_barrier();
         read_frags(g + 1, 0, b ^ 1);
       }
+      const int16_t_v zero = {};
 #pragma unroll
       for (int j = 0; j < MI; ++j)
 #pragma unroll
         for (int i = 0; i < NI; ++i)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xw[b][i], ya[b][j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xw[b][i], ya[b][j], FIRST && kk == 0 ? zero : acc[i][j],
+                                                            0, 0, 0);
 #pragma unroll
       for (int x = 0; x < NI + MI; ++x) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
@@ -915,32 +913,29 @@ __global__ __launch_bounds__(512, 1) void gemm_s8_persist_kernel(const GemmArgs 
       __builtin_amdgcn_sched_group_barrier(0x008, NI * MI - (NI + MI), 0);
     }
   };
-  for (int g = 0; g < total; ++g) {
+  for (int g = 0; g < total;) {
+    // one tile: KT slices, the first one peeled (it starts the accumulators from zero)
     if (g + 1 < total) issue();
-    slice(g);
-    if (++kt == KT) {
-      // Every wave has read all of slice g (barrier above): its slot is the staging area until the barrier below,
-      // after which slice g + 2 may load into it.
-      uint8_t* stage = wave < FIT ? smem + (g & 1) * STAGE + wave * SB : smem + 2 * STAGE + (wave - FIT) * SB;
-      // An opaque lane index keeps the epilogue's lane-derived offsets from being hoisted out of the tile loop,
-      // where they would hold registers through the main loop.
-      int el = lane;
-      asm volatile("" : "+v"(el));
-      store_epilogue<EPI, NI, MI>(acc, m0 + wm * WM, n0 + wn * WN, el, args, stage);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      __builtin_amdgcn_s_barrier();
-      // The next slice's first fragments again: the copies read above are dead on this path, so they do not stay
-      // live through the epilogue.
-      read_frags(g + 1, 0, 0);
-#pragma unroll
-      for (int i = 0; i < NI; ++i)
-#pragma unroll
-        for (int j = 0; j < MI; ++j)
-#pragma unroll
-          for (int q = 0; q < 16; ++q) acc[i][j][q] = 0;
-      kt = 0;
-      if (++r < my_tiles) coords(r, m0, n0);
+    slice(g, std::true_type{});
+    ++g;
+    for (int kt = 1; kt < KT; ++kt, ++g) {
+      if (g + 1 < total) issue();
+      slice(g, std::false_type{});
     }
+    // Every wave has read all of the tile's last slice g - 1 (barrier above): its slot is the staging area until
+    // the barrier below, after which slice g + 1 may load into it.
+    uint8_t* stage = wave < FIT ? smem + ((g - 1) & 1) * STAGE + wave * SB : smem + 2 * STAGE + (wave - FIT) * SB;
+    // An opaque lane index keeps the epilogue's lane-derived offsets from being hoisted out of the tile loop,
+    // where they would hold registers through the main loop.
+    int el = lane;
+    asm volatile("" : "+v"(el));
+    store_epilogue<EPI, NI, MI>(acc, m0 + wm * WM, n0 + wn * WN, el, args, stage);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    // The next slice's first fragments again: the copies read above are dead on this path, so they do not stay
+    // live through the epilogue.
+    read_frags(g, 0, 0);
+    if (++r < my_tiles) coords(r, m0, n0);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }

@@ -5,6 +5,8 @@
 //  * slot_weights: per token and pool head, the weights of M competing queries, softmax over the queries times
 //    sigmoid(logit + bias), written transposed (query-major rows over the tokens, the layout of the pooling product)
 //    with per-block sums over the tokens (each query's mass).
+#include <algorithm>
+
 #include "common.h"
 
 namespace ff {
@@ -55,6 +57,82 @@ __global__ __launch_bounds__(256) void layer_norm2_kernel(const half_t* __restri
 #pragma unroll
   for (int k = 0; k < PER; ++k)
     if (64 * k + lane < C) orow[64 * k + lane] = static_cast<half_t>(v[k]);
+}
+
+// The same two norms for C % 256 == 0 (Haruka's 768): lane l holds the 4 contiguous columns 4 (l + 64 k), so each
+// load and store moves 8 bytes per lane, and each wave streams rows (row = wave id + k * waves in the grid) with the
+// four affine vectors kept in registers. Same arithmetic as layer_norm2_kernel; only the order of the sums differs.
+template <int CH>
+__global__ __launch_bounds__(256) void layer_norm2_vec_kernel(const half_t* __restrict__ x, int64_t T, int C,
+                                                              const half_t* __restrict__ g1,
+                                                              const half_t* __restrict__ b1,
+                                                              const half_t* __restrict__ g2,
+                                                              const half_t* __restrict__ b2, float eps,
+                                                              half_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t waves = static_cast<int64_t>(gridDim.x) * 4;
+  const int nch = C / 256;  // chunks per lane (<= CH)
+  half4_t ga[CH], ba[CH], gb[CH], bb[CH];
+#pragma unroll
+  for (int k = 0; k < CH; ++k)
+    if (k < nch) {
+      const int c = 4 * (lane + 64 * k);
+      ga[k] = *reinterpret_cast<const half4_t*>(g1 + c);
+      ba[k] = *reinterpret_cast<const half4_t*>(b1 + c);
+      gb[k] = *reinterpret_cast<const half4_t*>(g2 + c);
+      bb[k] = *reinterpret_cast<const half4_t*>(b2 + c);
+    }
+  const float inv_c = 1.f / static_cast<float>(C);
+  for (int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); row < T; row += waves) {
+    const half_t* xr = x + row * C;
+    float v[CH][4];
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      half4_t h = {};
+      if (k < nch) h = *reinterpret_cast<const half4_t*>(xr + 4 * (lane + 64 * k));
+#pragma unroll
+      for (int t = 0; t < 4; ++t) v[k][t] = static_cast<float>(h[t]);
+    }
+    auto norm = [&](const half4_t (&g)[CH], const half4_t (&b)[CH], bool round_fp16) __attribute__((always_inline)) {
+      float s = 0.f;
+#pragma unroll
+      for (int k = 0; k < CH; ++k)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) s += v[k][t];
+#pragma unroll
+      for (int m = 32; m; m >>= 1) s += xor_shuffle(s, m);
+      const float mean = s * inv_c;
+      float q = 0.f;
+#pragma unroll
+      for (int k = 0; k < CH; ++k)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float d = k < nch ? v[k][t] - mean : 0.f;
+          q += d * d;
+        }
+#pragma unroll
+      for (int m = 32; m; m >>= 1) q += xor_shuffle(q, m);
+      const float rstd = 1.f / sqrtf(q * inv_c + eps);
+#pragma unroll
+      for (int k = 0; k < CH; ++k)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float y = (v[k][t] - mean) * rstd * static_cast<float>(g[k][t]) + static_cast<float>(b[k][t]);
+          v[k][t] = round_fp16 ? static_cast<float>(static_cast<half_t>(y)) : y;
+        }
+    };
+    norm(ga, ba, true);
+    norm(gb, bb, false);
+    half_t* orow = out + row * C;
+#pragma unroll
+    for (int k = 0; k < CH; ++k)
+      if (k < nch) {
+        half4_t h;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) h[t] = static_cast<half_t>(v[k][t]);
+        *reinterpret_cast<half4_t*>(orow + 4 * (lane + 64 * k)) = h;
+      }
+  }
 }
 
 // Tokens per workgroup of slot_weights.
@@ -131,10 +209,18 @@ extern "C" int ff_layer_norm2(const void* x, int64_t T, int64_t C, const void* g
   const auto *pg2 = static_cast<const half_t*>(g2), *pb2 = static_cast<const half_t*>(b2);
   auto* po = static_cast<half_t*>(out);
   const int Ci = static_cast<int>(C);
-  if (C <= 768)
+  const auto aligned8 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 8 == 0; };
+  const bool vec = C % 256 == 0 && C <= 1024 && aligned8(x) && aligned8(g1) && aligned8(b1) && aligned8(g2) &&
+                   aligned8(b2) && aligned8(out);
+  if (vec) {
+    // a few waves per SIMD stream the rows, so the affine vectors are loaded once per wave
+    const dim3 vgrid(static_cast<unsigned>(std::min<int64_t>((T + 3) / 4, 2048)));
+    layer_norm2_vec_kernel<4><<<vgrid, 256, 0, st>>>(px, T, Ci, pg1, pb1, pg2, pb2, eps, po);
+  } else if (C <= 768) {
     layer_norm2_kernel<12><<<grid, 256, 0, st>>>(px, T, Ci, pg1, pb1, pg2, pb2, eps, po);
-  else
+  } else {
     layer_norm2_kernel<32><<<grid, 256, 0, st>>>(px, T, Ci, pg1, pb1, pg2, pb2, eps, po);
+  }
   return check_launch("layer_norm2");
 }
 

@@ -307,15 +307,20 @@ def test_attention_identical_keys_give_mean_of_values(dev, rng):
 
 
 def test_layer_norm2_matches_two_float_layer_norms(dev, rng):
-    """ff_layer_norm2 against two float64 LayerNorms with the fp16 rounding between them (768 and 2048 columns)."""
+    """ff_layer_norm2 against two float64 LayerNorms with the fp16 rounding between them: the 8-byte-vector kernel
+    (C % 256 == 0 up to 1024, also with more rows than its grid has waves) and the per-column kernel (2048, 64, and
+    768 on a tensor that starts 2 bytes past an 8-byte boundary)."""
     from foidfinder_amd import kernels as K
 
-    for T, C in ((300, 768), (5, 2048), (1, 64)):
+    for T, C, shift in ((300, 768, 0), (8300, 768, 0), (7, 1024, 0), (3, 256, 0), (5, 2048, 0), (1, 64, 0),
+                        (9, 768, 1)):
         x = (rng.standard_normal((T, C)) * 3 + 0.5).astype(np.float16)
         g1, b1, g2, b2 = ((1 + 0.1 * rng.standard_normal(C)).astype(np.float16), (0.1 * rng.standard_normal(C)).astype(np.float16),
                           (1 + 0.1 * rng.standard_normal(C)).astype(np.float16), (0.1 * rng.standard_normal(C)).astype(np.float16))
+        xd = torch.empty(T * C + shift, dtype=torch.float16, device=dev)[shift:].view(T, C)
+        xd.copy_(to_gpu(x, dev))
         out = torch.empty(T, C, dtype=torch.float16, device=dev)
-        K.layer_norm2(*(to_gpu(a, dev) for a in (x, g1, b1, g2, b2)), 1e-6, out)
+        K.layer_norm2(xd, *(to_gpu(a, dev) for a in (g1, b1, g2, b2)), 1e-6, out)
         torch.cuda.synchronize()
 
         def ln(v, g, b):
