@@ -354,3 +354,32 @@ def test_slot_weights_matches_float(dev, rng, B, N, G, M, shared_c):
     assert np.abs(a_t.cpu().numpy().astype(np.float64) - want).max() < 1e-3
     mass = partial.sum(1).cpu().numpy().astype(np.float64)
     assert np.abs(mass - want.sum(-1)).max() < 1e-4 * N
+
+
+def test_empty_inputs_are_no_ops(dev):
+    """Zero tokens (or zero images) through every op: nothing is launched and the output buffers keep their bytes."""
+    from foidfinder_amd import kernels as K
+
+    f16, i8, f32 = torch.float16, torch.int8, torch.float32
+    x = torch.empty(0, 1024, dtype=f16, device=dev)
+    a8 = torch.empty(0, 1024, dtype=i8, device=dev)
+    rs = torch.empty(0, dtype=f32, device=dev)
+    K.rot_q8_1024(x, None, None, a8, rs)
+    K.rot_q8_h128(torch.empty(0, 2816, dtype=f16, device=dev), torch.empty(0, 2816, dtype=i8, device=dev), rs)
+    w = torch.ones(256, 1024, dtype=i8, device=dev)
+    ones = torch.ones(256, dtype=f32, device=dev)
+    K.gemm_s8(a8, w, rs, ones, ones, torch.empty(0, 256, dtype=f16, device=dev), K.EPI_BIAS_F16, 0, None, None, 1.0)
+    K.attention(torch.empty(0, 3 * 1024, dtype=f16, device=dev), torch.empty(0, 1024, dtype=f16, device=dev), 1025)
+    g = torch.ones(768, dtype=f16, device=dev)
+    K.layer_norm2(torch.empty(0, 768, dtype=f16, device=dev), g, g, g, g, 1e-6, torch.empty(0, 768, dtype=f16, device=dev))
+    sentinel = torch.full((0, 96, 10), 7.0, dtype=f16, device=dev)
+    K.slot_weights(torch.empty(0, 10, 96, dtype=f16, device=dev), torch.zeros(96, dtype=f32, device=dev),
+                   torch.zeros(6, dtype=f32, device=dev), 16, sentinel,
+                   torch.empty(0, K.slot_weights_blocks(10), 96, dtype=f32, device=dev))
+    # a real launch after the no-ops still works (nothing was left half-launched)
+    y = torch.randn(4, 1024, device=dev).half()
+    out = torch.empty(4, 1024, dtype=i8, device=dev)
+    r4 = torch.empty(4, dtype=f32, device=dev)
+    K.rot_q8_1024(y, None, None, out, r4)
+    torch.cuda.synchronize()
+    assert (r4 > 0).all()
