@@ -162,7 +162,9 @@ __device__ __forceinline__ void attention_block(const half_t* __restrict__ qkv, 
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
       one_last[kh][0] = static_cast<half_t>(1.f);
-      one_last[kh][1] = static_cast<half_t>((ntiles - 1) * BKV + kh * 32 + fr >= L ? 2.f : 0.f);
+      // key of this lane's row in the last tile: half kh (SPLIT: slot 0 is the wave's own half kh_sel)
+      const int key = (ntiles - 1) * BKV + (SPLIT ? kh_sel : kh) * 32 + fr;
+      one_last[kh][1] = static_cast<half_t>(key >= L ? 2.f : 0.f);
     }
     mq[1] = static_cast<half_t>(-65504.f);
   }
@@ -184,7 +186,7 @@ __device__ __forceinline__ void attention_block(const half_t* __restrict__ qkv, 
   // Half kh of the tile (SPLIT: slot 0 is the wave's own half, whose rows koff/voff already select)
   auto qk = [&](int kh, bool last) __attribute__((always_inline)) {
     const float16_t zero = {};
-    const half8_t ok = last ? one_last[SPLIT ? kh_sel : kh] : one_k;
+    const half8_t ok = last ? one_last[kh] : one_k;
     xs[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ok, mq, zero, 0, 0, 0);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
