@@ -1,5 +1,5 @@
 """Launches each block kernel at the batch-32 EVA02-L/14-448 shapes, plus a plain copy of known size, for hardware
-counter runs (one counter set per run):
+counter runs (one counter set per run; `--only` narrows the launches to some of them):
 
     rocprofv3 --pmc FETCH_SIZE -d <dir> -o fetch -- python -m foidfinder_amd.profile_kernels
     rocprofv3 --pmc WRITE_SIZE -d <dir> -o write -- python -m foidfinder_amd.profile_kernels
@@ -26,7 +26,9 @@ def main() -> None:
     ap.add_argument("--reps", type=int, default=3)
     ap.add_argument("--variants", default="qkv=8,proj=8,fc1=8,fc2=8",
                     help="GEMM tile variant per GEMM, as the engine's autotune picked them (bench.py prints them)")
+    ap.add_argument("--only", default="", help="comma-separated subset of: rot,gemm,attention,copy (default: all)")
     args = ap.parse_args()
+    only = set(args.only.split(",")) if args.only else {"rot", "gemm", "attention", "copy"}
     var = {kv.split("=")[0]: int(kv.split("=")[1]) for kv in args.variants.split(",")}
     k = kernels()
     dev = torch.device("cuda:0")
@@ -55,17 +57,21 @@ def main() -> None:
     src = torch.empty(COPY_BYTES // 2, device=dev, dtype=torch.half)
     dst = torch.empty_like(src)
     for _ in range(args.reps):
-        k.rot_q8_1024(x, ones(d), zeros(d), a8, rs, cfg.eps)
-        k.rot_q8_1024(o16, None, None, a8, rs, cfg.eps)
-        k.rot_q8_h128(h16, h8, rs, *pad_norm(ones(h), zeros(h), hp), h, cfg.eps)
-        k.gemm_s8(a8, w["qkv"], rs, cs["qkv"], zeros(3 * d), out_qkv, EPI_QKV_ROPE, var["qkv"], cos, sin, 0.18)
-        k.gemm_s8(a8, w["proj"], rs, cs["proj"], zeros(d), xr, EPI_RESIDUAL, var["proj"], None, None, 1.0)
-        k.gemm_s8(a8, w["fc1"], rs, cs["fc1"], zeros(2 * hp), hout, EPI_SWIGLU, var["fc1"], None, None, 1.0)
-        k.gemm_s8(h8, w["fc2"], rs, cs["fc2"], zeros(d), xr, EPI_RESIDUAL, var["fc2"], None, None, 1.0)
-        k.attention(qkv, o16, cfg.tokens)
-        dst.copy_(src)
+        if "rot" in only:
+            k.rot_q8_1024(x, ones(d), zeros(d), a8, rs, cfg.eps)
+            k.rot_q8_1024(o16, None, None, a8, rs, cfg.eps)
+            k.rot_q8_h128(h16, h8, rs, *pad_norm(ones(h), zeros(h), hp), h, cfg.eps)
+        if "gemm" in only:
+            k.gemm_s8(a8, w["qkv"], rs, cs["qkv"], zeros(3 * d), out_qkv, EPI_QKV_ROPE, var["qkv"], cos, sin, 0.18)
+            k.gemm_s8(a8, w["proj"], rs, cs["proj"], zeros(d), xr, EPI_RESIDUAL, var["proj"], None, None, 1.0)
+            k.gemm_s8(a8, w["fc1"], rs, cs["fc1"], zeros(2 * hp), hout, EPI_SWIGLU, var["fc1"], None, None, 1.0)
+            k.gemm_s8(h8, w["fc2"], rs, cs["fc2"], zeros(d), xr, EPI_RESIDUAL, var["fc2"], None, None, 1.0)
+        if "attention" in only:
+            k.attention(qkv, o16, cfg.tokens)
+        if "copy" in only:
+            dst.copy_(src)
     torch.cuda.synchronize()
-    print(f"profile_kernels: {args.reps} reps at batch {args.batch} (M = {M}), GEMM variants {var}; copy of "
+    print(f"profile_kernels: {sorted(only)} x {args.reps} at batch {args.batch} (M = {M}), GEMM variants {var}; copy of "
           f"{COPY_BYTES} bytes", flush=True)
 
 
