@@ -940,8 +940,105 @@ __global__ __launch_bounds__(512, 1) void gemm_s8_persist_kernel(const GemmArgs 
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-static int launch_persist(const GemmArgs& a, int epi, hipStream_t st) {
-  if (a.K % 128 != 0) return fail(FF_EINVAL, "gemm_s8: K must be a multiple of the slice");
+// ---------------- the rows past the last whole 256-row tile (variant 8) ----------------
+//
+// M = 32 800 leaves 32 rows past 128 whole row tiles. As one more 256-row tile per column tile they would take a
+// whole extra round of the persistent grid (4 tiles on 4 CUs for N = 1024, each with the full K loop: ~24 us of
+// fc2's ~113 us). Here each workgroup takes 32 of those rows x 32 columns and splits K over its 8 waves: every wave
+// loads its K range straight into registers (buffer loads: rows past M or N read zeros), runs its MFMAs, and the
+// int32 partial products are summed exactly through LDS; wave 0 then applies the same epilogue as the main kernel.
+constexpr int T_NI = 1;  // 32-column blocks per workgroup: more, narrower workgroups spread the rows' loads over CUs
+
+// KB: k-steps per load batch, at least a wave's share of K when that is at most 12 k-steps (K <= 3072), so that
+// all of a wave's loads are in flight at once.
+template <int EPI, int KB>
+__global__ __launch_bounds__(512) void gemm_s8_tail_kernel(const GemmArgs args, int m_first) {
+  __shared__ __attribute__((aligned(16))) int red[8 * 64 * 16 * T_NI];  // [wave][lane][accumulators]
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int fr = lane & 31, fk = lane >> 5;
+  const int M = args.M, N = args.N, K = args.K;
+  const int m0 = m_first + 32 * static_cast<int>(blockIdx.y), n0 = 32 * T_NI * static_cast<int>(blockIdx.x);
+  const int ks = K / 32, k_lo = wave * ks / 8, k_hi = (wave + 1) * ks / 8;
+  const int a_bytes = buf_bytes(static_cast<int64_t>(M - m0) * K), w_bytes = buf_bytes(static_cast<int64_t>(N - n0) * K);
+  const int8_t* abase = args.A + static_cast<int64_t>(m0) * K;
+  const int8_t* wbase = args.W + static_cast<int64_t>(n0) * K;
+  int16_t_v acc[T_NI][1] = {};
+  for (int kb = k_lo; kb < k_hi; kb += KB) {
+    int4_t xw[KB][T_NI], ya[KB];
+#pragma unroll
+    for (int u = 0; u < KB; ++u) {
+      const uint32_t kofs = static_cast<uint32_t>(32 * (kb + u) + 16 * fk);
+      const bool in = kb + u < k_hi;  // wave-uniform
+      ya[u] = in ? __builtin_bit_cast(int4_t, buf_load_f4(abase, a_bytes, static_cast<uint32_t>(fr * K) + kofs))
+                 : int4_t{};
+#pragma unroll
+      for (int i = 0; i < T_NI; ++i)
+        xw[u][i] = in ? __builtin_bit_cast(int4_t, buf_load_f4(wbase, w_bytes,
+                                                               static_cast<uint32_t>((32 * i + fr) * K) + kofs))
+                      : int4_t{};
+    }
+#pragma unroll
+    for (int u = 0; u < KB; ++u)
+#pragma unroll
+      for (int i = 0; i < T_NI; ++i)
+        acc[i][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xw[u][i], ya[u], acc[i][0], 0, 0, 0);
+  }
+  int* mine = red + (wave * 64 + lane) * 16 * T_NI;
+#pragma unroll
+  for (int i = 0; i < T_NI; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<int4_t*>(mine + 16 * i + 4 * q) =
+          int4_t{acc[i][0][4 * q], acc[i][0][4 * q + 1], acc[i][0][4 * q + 2], acc[i][0][4 * q + 3]};
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll 1
+  for (int w = 1; w < 8; ++w) {
+    const int* theirs = red + (w * 64 + lane) * 16 * T_NI;
+#pragma unroll
+    for (int i = 0; i < T_NI; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int4_t v = *reinterpret_cast<const int4_t*>(theirs + 16 * i + 4 * q);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[i][0][4 * q + t] += v[t];
+      }
+  }
+  // every partial product is in wave 0's registers now (the other waves have left): `red` is its staging area
+  static_assert(stage_bytes<FF_EPI_QKV_ROPE, T_NI>() <= 8 * 64 * 16 * T_NI * 4, "staging must fit in the reduction area");
+  store_epilogue<EPI, T_NI, 1>(acc, m0, n0, lane, args, reinterpret_cast<uint8_t*>(red));
+}
+
+template <int KB>
+static int launch_tail_kb(const GemmArgs& a, int m_first, int epi, hipStream_t st) {
+  const int rows = a.M - m_first;
+  const dim3 grid(static_cast<unsigned>((a.N + 32 * T_NI - 1) / (32 * T_NI)), static_cast<unsigned>((rows + 31) / 32));
+  switch (epi) {
+    case FF_EPI_QKV_ROPE: gemm_s8_tail_kernel<FF_EPI_QKV_ROPE, KB><<<grid, 512, 0, st>>>(a, m_first); break;
+    case FF_EPI_RESIDUAL: gemm_s8_tail_kernel<FF_EPI_RESIDUAL, KB><<<grid, 512, 0, st>>>(a, m_first); break;
+    case FF_EPI_GELU_F16: gemm_s8_tail_kernel<FF_EPI_GELU_F16, KB><<<grid, 512, 0, st>>>(a, m_first); break;
+    case FF_EPI_SWIGLU: gemm_s8_tail_kernel<FF_EPI_SWIGLU, KB><<<grid, 512, 0, st>>>(a, m_first); break;
+    case FF_EPI_BIAS_F16: gemm_s8_tail_kernel<FF_EPI_BIAS_F16, KB><<<grid, 512, 0, st>>>(a, m_first); break;
+    case FF_EPI_I32: gemm_s8_tail_kernel<FF_EPI_I32, KB><<<grid, 512, 0, st>>>(a, m_first); break;
+    default: return fail(FF_EINVAL, "gemm_s8: bad epilogue");
+  }
+  return check_launch("gemm_s8");
+}
+
+static int launch_tail(const GemmArgs& a, int m_first, int epi, hipStream_t st) {
+  const int per_wave = (a.K / 32 + 7) / 8;  // k-steps of a wave's share of K
+  if (per_wave <= 4) return launch_tail_kb<4>(a, m_first, epi, st);
+  if (per_wave <= 8) return launch_tail_kb<8>(a, m_first, epi, st);
+  return launch_tail_kb<12>(a, m_first, epi, st);
+}
+
+static int launch_persist(const GemmArgs& args, int epi, hipStream_t st) {
+  if (args.K % 128 != 0) return fail(FF_EINVAL, "gemm_s8: K must be a multiple of the slice");
+  // Whole 256-row tiles on the persistent grid; the rows past them (if any) on the tail kernel, after it.
+  const int whole = args.M / 256 * 256;
+  const bool split = whole > 0 && whole < args.M;
+  GemmArgs a = args;
+  if (split) a.M = whole;
   const int64_t tiles = static_cast<int64_t>((a.M + 255) / 256) * ((a.N + 255) / 256);
   if (tiles > 0x7fffffff) return fail(FF_EINVAL, "gemm_s8: too many tiles");
   const void* kernels[] = {
@@ -964,7 +1061,8 @@ static int launch_persist(const GemmArgs& a, int epi, hipStream_t st) {
     case FF_EPI_I32: gemm_s8_persist_kernel<FF_EPI_I32><<<grid, 512, 0, st>>>(a); break;
     default: return fail(FF_EINVAL, "gemm_s8: bad epilogue");
   }
-  return check_launch("gemm_s8");
+  if (const int rc = check_launch("gemm_s8"); rc != FF_OK || !split) return rc;
+  return launch_tail(args, whole, epi, st);
 }
 
 // ---------------- variants 2, 3: register-staged double buffering ----------------

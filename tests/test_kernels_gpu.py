@@ -147,7 +147,8 @@ def run_gemm(dev, a, w, rs, cs, bias, epi, variant, out=None, rope=None, q_scale
 
 
 GEMM_VARIANTS = [1, 2, 3, 4, 5, 6, 7, 8]  # ff_gemm_s8_variants()
-GEMM_SHAPES = [(1, 16, 64), (17, 48, 128), (300, 3072, 1024), (1025, 5632, 1024), (129, 1024, 2816), (257, 272, 192)]
+GEMM_SHAPES = [(1, 16, 64), (17, 48, 128), (300, 3072, 1024), (1025, 5632, 1024), (129, 1024, 2816), (257, 272, 192),
+               (300, 1024, 2816)]
 
 
 def test_gemm_variant_list_is_complete(dev):
