@@ -944,92 +944,92 @@ __global__ __launch_bounds__(512, 1) void gemm_s8_persist_kernel(const GemmArgs 
 //
 // M = 32 800 leaves 32 rows past 128 whole row tiles. As one more 256-row tile per column tile they would take a
 // whole extra round of the persistent grid (4 tiles on 4 CUs for N = 1024, each with the full K loop: ~24 us of
-// fc2's ~113 us). Here each workgroup takes 32 of those rows x 32 columns and splits K over its 8 waves: every wave
-// loads its K range straight into registers (buffer loads: rows past M or N read zeros), runs its MFMAs, and the
-// int32 partial products are summed exactly through LDS; wave 0 then applies the same epilogue as the main kernel.
-constexpr int T_NI = 1;  // 32-column blocks per workgroup: more, narrower workgroups spread the rows' loads over CUs
+// fc2's ~113 us). Here each workgroup takes 32 of those rows x 32 columns and splits K over its 8 waves in 128-byte
+// chunks (wave w: chunks w, w + 8, ...). A wave stages each chunk of its 32 A rows and 32 W rows in its own two LDS
+// buffers with buffer->LDS loads (whole 128-byte rows per 8 lanes, the next chunk loading while the current one is
+// multiplied; rows past M or N read as zeros), the waves' int32 partial products are summed exactly through LDS, and
+// wave 0 applies the same epilogue as the main kernel. No barrier until the sum: each wave touches only its buffers.
+constexpr int T_CHUNK = 64 * 128;  // one staged chunk: 32 A rows + 32 W rows x 128 K bytes
 
-// KB: k-steps per load batch, at least a wave's share of K when that is at most 12 k-steps (K <= 3072), so that
-// all of a wave's loads are in flight at once.
-template <int EPI, int KB>
+template <int EPI>
 __global__ __launch_bounds__(512) void gemm_s8_tail_kernel(const GemmArgs args, int m_first) {
-  __shared__ __attribute__((aligned(16))) int red[8 * 64 * 16 * T_NI];  // [wave][lane][accumulators]
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[8 * 2 * T_CHUNK];  // [wave][2 buffers][64 rows x 128 B]
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int fr = lane & 31, fk = lane >> 5;
-  const int M = args.M, N = args.N, K = args.K;
-  const int m0 = m_first + 32 * static_cast<int>(blockIdx.y), n0 = 32 * T_NI * static_cast<int>(blockIdx.x);
-  const int ks = K / 32, k_lo = wave * ks / 8, k_hi = (wave + 1) * ks / 8;
+  const int M = args.M, N = args.N, K = args.K, nch = K / 128;
+  const int m0 = m_first + 32 * static_cast<int>(blockIdx.y), n0 = 32 * static_cast<int>(blockIdx.x);
   const int a_bytes = buf_bytes(static_cast<int64_t>(M - m0) * K), w_bytes = buf_bytes(static_cast<int64_t>(N - n0) * K);
   const int8_t* abase = args.A + static_cast<int64_t>(m0) * K;
   const int8_t* wbase = args.W + static_cast<int64_t>(n0) * K;
-  int16_t_v acc[T_NI][1] = {};
-  for (int kb = k_lo; kb < k_hi; kb += KB) {
-    int4_t xw[KB][T_NI], ya[KB];
+  uint8_t* mine = lds + wave * 2 * T_CHUNK;
+  // Load p of a chunk fills LDS rows 8p .. 8p + 7 (rows 0-31: A, 32-63: W); lane l writes physical 16-byte slot l % 8
+  // of row 8p + l / 8, so it fetches the global chunk that the swizzle of wswz<128> puts there.
+  auto load_chunk = [&](int c, uint8_t* dst) __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < KB; ++u) {
-      const uint32_t kofs = static_cast<uint32_t>(32 * (kb + u) + 16 * fk);
-      const bool in = kb + u < k_hi;  // wave-uniform
-      ya[u] = in ? __builtin_bit_cast(int4_t, buf_load_f4(abase, a_bytes, static_cast<uint32_t>(fr * K) + kofs))
-                 : int4_t{};
-#pragma unroll
-      for (int i = 0; i < T_NI; ++i)
-        xw[u][i] = in ? __builtin_bit_cast(int4_t, buf_load_f4(wbase, w_bytes,
-                                                               static_cast<uint32_t>((32 * i + fr) * K) + kofs))
-                      : int4_t{};
+    for (int p = 0; p < 8; ++p) {
+      const int row = 8 * p + (lane >> 3), slot = lane & 7;
+      const uint32_t voff =
+          static_cast<uint32_t>((row & 31) * K + c * 128 + ((slot ^ ((row >> 1) & 7)) << 4));
+      if (p < 4)
+        buffer_to_lds(abase, a_bytes, dst + p * 1024, voff);
+      else
+        buffer_to_lds(wbase, w_bytes, dst + p * 1024, voff);
     }
+  };
+  int16_t_v acc[1][1] = {};
+  int b = 0;
+  if (wave < nch) load_chunk(wave, mine);
+  for (int c = wave; c < nch; c += 8, b ^= 1) {
+    if (c + 8 < nch) {
+      load_chunk(c + 8, mine + (b ^ 1) * T_CHUNK);  // that buffer's last reads finished in the previous chunk
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // chunk c has landed (only chunk c + 8's loads outstanding)
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    const uint8_t* sb = mine + b * T_CHUNK;
 #pragma unroll
-    for (int u = 0; u < KB; ++u)
-#pragma unroll
-      for (int i = 0; i < T_NI; ++i)
-        acc[i][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xw[u][i], ya[u], acc[i][0], 0, 0, 0);
+    for (int kk = 0; kk < 4; ++kk) {
+      const int4_t ya = *reinterpret_cast<const int4_t*>(sb + wswz<128>(fr, 2 * kk + fk));
+      const int4_t xw = *reinterpret_cast<const int4_t*>(sb + wswz<128>(32 + fr, 2 * kk + fk));
+      acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xw, ya, acc[0][0], 0, 0, 0);
+    }
   }
-  int* mine = red + (wave * 64 + lane) * 16 * T_NI;
+  // partial products: each wave into the start of its own buffers (its chunk reads are done)
+  int* part = reinterpret_cast<int*>(mine) + lane * 16;
 #pragma unroll
-  for (int i = 0; i < T_NI; ++i)
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      *reinterpret_cast<int4_t*>(mine + 16 * i + 4 * q) =
-          int4_t{acc[i][0][4 * q], acc[i][0][4 * q + 1], acc[i][0][4 * q + 2], acc[i][0][4 * q + 3]};
+  for (int q = 0; q < 4; ++q)
+    *reinterpret_cast<int4_t*>(part + 4 * q) =
+        int4_t{acc[0][0][4 * q], acc[0][0][4 * q + 1], acc[0][0][4 * q + 2], acc[0][0][4 * q + 3]};
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll 1
   for (int w = 1; w < 8; ++w) {
-    const int* theirs = red + (w * 64 + lane) * 16 * T_NI;
+    const int* theirs = reinterpret_cast<const int*>(lds + w * 2 * T_CHUNK) + lane * 16;
 #pragma unroll
-    for (int i = 0; i < T_NI; ++i)
+    for (int q = 0; q < 4; ++q) {
+      const int4_t v = *reinterpret_cast<const int4_t*>(theirs + 4 * q);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int4_t v = *reinterpret_cast<const int4_t*>(theirs + 16 * i + 4 * q);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) acc[i][0][4 * q + t] += v[t];
-      }
+      for (int t = 0; t < 4; ++t) acc[0][0][4 * q + t] += v[t];
+    }
   }
-  // every partial product is in wave 0's registers now (the other waves have left): `red` is its staging area
-  static_assert(stage_bytes<FF_EPI_QKV_ROPE, T_NI>() <= 8 * 64 * 16 * T_NI * 4, "staging must fit in the reduction area");
-  store_epilogue<EPI, T_NI, 1>(acc, m0, n0, lane, args, reinterpret_cast<uint8_t*>(red));
-}
-
-template <int KB>
-static int launch_tail_kb(const GemmArgs& a, int m_first, int epi, hipStream_t st) {
-  const int rows = a.M - m_first;
-  const dim3 grid(static_cast<unsigned>((a.N + 32 * T_NI - 1) / (32 * T_NI)), static_cast<unsigned>((rows + 31) / 32));
-  switch (epi) {
-    case FF_EPI_QKV_ROPE: gemm_s8_tail_kernel<FF_EPI_QKV_ROPE, KB><<<grid, 512, 0, st>>>(a, m_first); break;
-    case FF_EPI_RESIDUAL: gemm_s8_tail_kernel<FF_EPI_RESIDUAL, KB><<<grid, 512, 0, st>>>(a, m_first); break;
-    case FF_EPI_GELU_F16: gemm_s8_tail_kernel<FF_EPI_GELU_F16, KB><<<grid, 512, 0, st>>>(a, m_first); break;
-    case FF_EPI_SWIGLU: gemm_s8_tail_kernel<FF_EPI_SWIGLU, KB><<<grid, 512, 0, st>>>(a, m_first); break;
-    case FF_EPI_BIAS_F16: gemm_s8_tail_kernel<FF_EPI_BIAS_F16, KB><<<grid, 512, 0, st>>>(a, m_first); break;
-    case FF_EPI_I32: gemm_s8_tail_kernel<FF_EPI_I32, KB><<<grid, 512, 0, st>>>(a, m_first); break;
-    default: return fail(FF_EINVAL, "gemm_s8: bad epilogue");
-  }
-  return check_launch("gemm_s8");
+  // every partial product is in wave 0's registers now: its own buffers are the epilogue's staging area
+  static_assert(stage_bytes<FF_EPI_QKV_ROPE, 1>() <= 2 * T_CHUNK, "staging must fit in wave 0's buffers");
+  store_epilogue<EPI, 1, 1>(acc, m0, n0, lane, args, lds);
 }
 
 static int launch_tail(const GemmArgs& a, int m_first, int epi, hipStream_t st) {
-  const int per_wave = (a.K / 32 + 7) / 8;  // k-steps of a wave's share of K
-  if (per_wave <= 4) return launch_tail_kb<4>(a, m_first, epi, st);
-  if (per_wave <= 8) return launch_tail_kb<8>(a, m_first, epi, st);
-  return launch_tail_kb<12>(a, m_first, epi, st);
+  const int rows = a.M - m_first;
+  const dim3 grid(static_cast<unsigned>((a.N + 31) / 32), static_cast<unsigned>((rows + 31) / 32));
+  switch (epi) {
+    case FF_EPI_QKV_ROPE: gemm_s8_tail_kernel<FF_EPI_QKV_ROPE><<<grid, 512, 0, st>>>(a, m_first); break;
+    case FF_EPI_RESIDUAL: gemm_s8_tail_kernel<FF_EPI_RESIDUAL><<<grid, 512, 0, st>>>(a, m_first); break;
+    case FF_EPI_GELU_F16: gemm_s8_tail_kernel<FF_EPI_GELU_F16><<<grid, 512, 0, st>>>(a, m_first); break;
+    case FF_EPI_SWIGLU: gemm_s8_tail_kernel<FF_EPI_SWIGLU><<<grid, 512, 0, st>>>(a, m_first); break;
+    case FF_EPI_BIAS_F16: gemm_s8_tail_kernel<FF_EPI_BIAS_F16><<<grid, 512, 0, st>>>(a, m_first); break;
+    case FF_EPI_I32: gemm_s8_tail_kernel<FF_EPI_I32><<<grid, 512, 0, st>>>(a, m_first); break;
+    default: return fail(FF_EINVAL, "gemm_s8: bad epilogue");
+  }
+  return check_launch("gemm_s8");
 }
 
 static int launch_persist(const GemmArgs& args, int epi, hipStream_t st) {
