@@ -1215,6 +1215,9 @@ extern "C" int ff_gemm_s8(const int8_t* A, const int8_t* W, int64_t M, int64_t N
   if (K % 64 != 0) return fail(FF_EINVAL, "gemm_s8: K must be a multiple of 64");
   if (N % 16 != 0) return fail(FF_EINVAL, "gemm_s8: N must be a multiple of 16");
   if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return fail(FF_EINVAL, "gemm_s8: dimension too large");
+  // offsets inside a tile's 256 rows of A or W (and of the output) are 32-bit byte offsets
+  if (K > (int64_t(1) << 22) || N > (int64_t(1) << 21))
+    return fail(FF_EINVAL, "gemm_s8: K above 2^22 or N above 2^21 is not supported");
   if (epi < FF_EPI_QKV_ROPE || epi > FF_EPI_I32) return fail(FF_EINVAL, "gemm_s8: bad epilogue");
   if (variant < 0 || variant > kVariants) return fail(FF_EINVAL, "gemm_s8: bad variant");
   if (epi == FF_EPI_QKV_ROPE) {

@@ -77,6 +77,8 @@ def test_gemm_s8_rejects_bad_arguments():
     assert "RoPE" in call(N=192, epi=0)[1]
     assert call(M=0) == (FF_OK, "")
     assert "misaligned" in call(ptrs=8)[1]
+    assert "not supported" in call(Kd=(1 << 22) + 64)[1]  # 32-bit offsets within a tile
+    assert "not supported" in call(N=(1 << 21) + 16)[1]
 
 
 def test_attention_rejects_bad_arguments():
