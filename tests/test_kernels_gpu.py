@@ -384,3 +384,35 @@ def test_empty_inputs_are_no_ops(dev):
     K.rot_q8_1024(y, None, None, out, r4)
     torch.cuda.synchronize()
     assert (r4 > 0).all()
+
+
+# The persistent variant sends the rows past its last whole 256-row tile to a split-K tail kernel (32 x 32 output
+# blocks, K in 128-byte chunks over 8 waves): tails of 1 .. 255 rows, a last column block of 16 columns, fewer K
+# chunks than waves and more.
+@pytest.mark.parametrize(("M", "N", "K"), [(511, 272, 384), (257, 96, 128), (288, 3072, 2816), (767, 5632, 1024)])
+def test_gemm_s8_tail_rows_int32_bit_exact(dev, rng, M, N, K):
+    a, w, rs, cs, bias = gemm_inputs(rng, M, N, K)
+    got = run_gemm(dev, a, w, rs, cs, bias, OG.EPI_I32, 8)
+    want = OG.gemm_s8_i32(a, w)
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[:4].tolist()}: {got[tuple(bad[0])]} vs {want[tuple(bad[0])]}"
+
+
+@pytest.mark.parametrize("epi", [OG.EPI_BIAS_F16, OG.EPI_RESIDUAL, OG.EPI_QKV_ROPE, OG.EPI_SWIGLU])
+def test_gemm_s8_tail_rows_epilogues(dev, rng, epi):
+    M, N, K = {OG.EPI_QKV_ROPE: (383, 3072, 256), OG.EPI_SWIGLU: (300, 5632, 384)}.get(epi, (511, 272, 384))
+    a, w, rs, cs, bias = gemm_inputs(rng, M, N, K)
+    kw, out, rope = {}, None, None
+    if epi == OG.EPI_RESIDUAL:
+        out = rng.standard_normal((M, N)).astype(np.float16)
+        kw["residual"] = out
+    if epi == OG.EPI_QKV_ROPE:
+        rope = OM.eva02_rope_tables(32, 16)
+        kw.update(rope_cos=rope[0], rope_sin=rope[1], q_scale=OM.Q_SCALE)
+    got = run_gemm(dev, a, w, rs, cs, bias, epi, 8, out=out, rope=rope, q_scale=kw.get("q_scale", 1.0))
+    want = OG.gemm_s8(a, w, rs, cs, bias, epi, **kw)
+    if epi == OG.EPI_SWIGLU:
+        assert_within_one_fp16_ulp(got, want, "SwiGLU epilogue, tail rows")
+        return
+    bad = np.argwhere(got.view(np.uint16) != want.view(np.uint16))
+    assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[:4].tolist()}: {got[tuple(bad[0])]} vs {want[tuple(bad[0])]}"
