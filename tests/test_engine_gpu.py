@@ -145,3 +145,25 @@ def test_engine_full_eva02_l_wiring(dev):
     _, state = raw_and_converted(cfg, seed=3)
     images = OM.synthetic_images(1, cfg.img_size, seed=8)
     check_wiring(Eva02Int8(state, cfg, device=dev), state, cfg, images, dev)
+
+
+def test_full_size_batch_32_is_permutation_equivariant(dev):
+    """The benchmark's configuration itself (EVA02-L/14-448, batch 32) through properties that hold at any size:
+    every block kernel works row by row (GEMMs exact in int32, rotations per token) or sequence by sequence
+    (attention), and the stem and head GEMMs see the same shapes, so permuting the batch permutes the logits bit for
+    bit; and the graph replay equals the eager forward bit for bit. (A batch of 1 against a batch of 32 is not
+    compared: the third-party stem and head GEMMs pick their algorithm by M, which may round differently.)"""
+    from foidfinder_amd.engine import Eva02Config, Eva02Int8
+
+    cfg = Eva02Config()
+    _, state = raw_and_converted(cfg, seed=4)
+    eng = Eva02Int8(state, cfg, device=dev)
+    images = torch.from_numpy(OM.synthetic_images(32, cfg.img_size, seed=9)).to(dev)
+    full = eng(images).clone()
+    torch.cuda.synchronize()
+    assert torch.isfinite(full).all()
+    assert torch.equal(eng.eager(images), full), "graph replay differs from eager at batch 32"
+    perm = torch.randperm(32, generator=torch.Generator().manual_seed(0)).to(dev)
+    shuffled = eng(images[perm].contiguous()).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(shuffled, full[perm]), "permuting the batch does not permute the logits"
