@@ -45,4 +45,28 @@ __device__ __forceinline__ int xcd_remap(int b, int nblocks) {
 // Value of lane (lane ^ mask) within the wave (ds_bpermute).
 __device__ __forceinline__ float xor_shuffle(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
+// DPP controls: partner lane l ^ 1, l ^ 3 (quad_perm), l ^ 7 (row_half_mirror), l ^ 15 (row_mirror).
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR3 = 0x1B, DPP_XOR7 = 0x141, DPP_XOR15 = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Value of lane l ^ 16 within a 32-lane group (ds_swizzle bitmask mode: and 0x1F, or 0, xor 0x10).
+__device__ __forceinline__ float swz_xor16(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+
+// Sum over the 64 lanes, in every lane: within each 32-lane half by one swizzle and four DPP steps (partners l ^ 16,
+// ^ 15, ^ 7, ^ 3, ^ 1 cover all 32), then across the halves by one permute.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = v + swz_xor16(v);
+  v = v + dpp<DPP_XOR15>(v);
+  v = v + dpp<DPP_XOR7>(v);
+  v = v + dpp<DPP_XOR3>(v);
+  v = v + dpp<DPP_XOR1>(v);
+  return v + xor_shuffle(v, 32);
+}
+
 }  // namespace ff

@@ -83,24 +83,29 @@ __global__ __launch_bounds__(256) void layer_norm2_vec_kernel(const half_t* __re
       bb[k] = *reinterpret_cast<const half4_t*>(b2 + c);
     }
   const float inv_c = 1.f / static_cast<float>(C);
-  for (int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); row < T; row += waves) {
-    const half_t* xr = x + row * C;
+  // the next row's loads are issued before the current row's reductions, so a wave always has a row in flight
+  half4_t nxt[CH];
+  auto load = [&](int64_t r) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < CH; ++k)
+      nxt[k] = k < nch ? *reinterpret_cast<const half4_t*>(x + r * C + 4 * (lane + 64 * k)) : half4_t{};
+  };
+  int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row < T) load(row);
+  for (; row < T; row += waves) {
     float v[CH][4];
 #pragma unroll
-    for (int k = 0; k < CH; ++k) {
-      half4_t h = {};
-      if (k < nch) h = *reinterpret_cast<const half4_t*>(xr + 4 * (lane + 64 * k));
+    for (int k = 0; k < CH; ++k)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) v[k][t] = static_cast<float>(h[t]);
-    }
+      for (int t = 0; t < 4; ++t) v[k][t] = static_cast<float>(nxt[k][t]);
+    if (row + waves < T) load(row + waves);
     auto norm = [&](const half4_t (&g)[CH], const half4_t (&b)[CH], bool round_fp16) __attribute__((always_inline)) {
       float s = 0.f;
 #pragma unroll
       for (int k = 0; k < CH; ++k)
 #pragma unroll
         for (int t = 0; t < 4; ++t) s += v[k][t];
-#pragma unroll
-      for (int m = 32; m; m >>= 1) s += xor_shuffle(s, m);
+      s = wave_sum(s);
       const float mean = s * inv_c;
       float q = 0.f;
 #pragma unroll
@@ -110,8 +115,7 @@ __global__ __launch_bounds__(256) void layer_norm2_vec_kernel(const half_t* __re
           const float d = k < nch ? v[k][t] - mean : 0.f;
           q += d * d;
         }
-#pragma unroll
-      for (int m = 32; m; m >>= 1) q += xor_shuffle(q, m);
+      q = wave_sum(q);
       const float rstd = 1.f / sqrtf(q * inv_c + eps);
 #pragma unroll
       for (int k = 0; k < CH; ++k)

@@ -24,19 +24,6 @@
 
 namespace ff {
 
-// DPP controls: partner lane l ^ 1, l ^ 3 (quad_perm), l ^ 7 (row_half_mirror), l ^ 15 (row_mirror).
-constexpr int DPP_XOR1 = 0xB1, DPP_XOR3 = 0x1B, DPP_XOR7 = 0x141, DPP_XOR15 = 0x140;
-
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-
-// Value of lane l ^ 16 within a 32-lane group (ds_swizzle bitmask mode: and 0x1F, or 0, xor 0x10).
-__device__ __forceinline__ float swz_xor16(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
-}
-
 // Sign-tracked butterfly across lanes, u = fma(p, s, u) with partner p, own u, s = +1 (column bit 0) or -1 (column
 // bit 1), as one v_fmac_f32_dpp (DPP on the multiplicand: the partner's u). The compiler only emits it as
 // v_mov_b32_dpp + v_fmac_f32, so it is written out; one stage is one call over all of a lane's values, which are
@@ -91,12 +78,6 @@ __device__ __forceinline__ float add_h(uint32_t h2, float s) {
 __device__ __forceinline__ void bfly0_h(uint32_t h2, float& lo_plus_hi, float& lo_minus_hi) {
   asm("v_fma_mix_f32 %0, %1, 1.0, %1 op_sel:[0,0,1] op_sel_hi:[1,0,1]" : "=v"(lo_plus_hi) : "v"(h2));
   asm("v_fma_mix_f32 %0, %1, -1.0, %1 op_sel:[1,0,0] op_sel_hi:[1,0,1]" : "=v"(lo_minus_hi) : "v"(h2));
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m; m >>= 1) v = v + xor_shuffle(v, m);
-  return v;
 }
 
 __device__ __forceinline__ float wave_max(float v) {
