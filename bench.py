@@ -8,7 +8,8 @@ captured graph: patch-embed GEMM, 24 int8 blocks (3x rotate+quant 1024, rotate+q
 with fused epilogues, flash attention), final LayerNorm, 1024 -> 30877 tag GEMM. Weights are random-init (seeded).
 
 Prints one JSON line: images/s (whole job), per-kernel times measured live with HIP events on the launch stream,
-the roofline of the dominant kernel, and the CPU baseline (the numpy oracle's int8 forward on a bounded sample).
+the roofline of the dominant kernel, and the CPU baseline on the host's cores (PyTorch fp32 float forward at batch 2,
+the single W8A8 linear, and the numpy oracle's int8 forward of one image).
 """
 
 from __future__ import annotations
@@ -108,27 +109,87 @@ def kernel_table(eng, B: int, buf) -> dict:
     return out
 
 
-def cpu_baseline(state, cfg, n_images: int) -> dict:
-    """The numpy oracle's int8-semantics forward (a port of the reference's int8 path) on n_images images."""
-    import numpy as np
+def cpu_threads() -> int:
+    """Host threads for the CPU baseline: every core this process may use, capped by OMP_NUM_THREADS when set (a
+    shared host gives each GPU job a share of its cores and says so there)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(n, int(cap))) if cap.isdigit() else n
 
+
+def cpu_info() -> dict:
+    """lscpu's model name and sockets x cores per socket (x threads per core)."""
+    import subprocess
+
+    info = {}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            info[k.strip()] = v.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return {"model": info.get("Model name"),
+            "sockets_x_cores": f"{info.get('Socket(s)')} x {info.get('Core(s) per socket')} "
+                               f"(x {info.get('Thread(s) per core')} threads)"}
+
+
+def median_time(fn, runs: int = 3) -> float:
+    """1 untimed warm-up, then the median wall time of `runs` calls (s)."""
+    fn()
+    ts = []
+    for _ in range(runs):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return sorted(ts)[len(ts) // 2]
+
+
+def cpu_baseline(raw, state, cfg, n_images: int) -> dict:
+    """The CPU baseline on this host's cores, three legs:
+
+    - value: the EVA02-L/14-448 float forward in PyTorch fp32 on the CPU, in the op order of the reference's PyTorch
+      model (foidfinder/backends/cuda/reference.py:109-131, adapted to EVA02), batch 2, 1 warm-up + median of 3;
+    - w8a8_linear: the plumbing config's single W8A8 linear (1025 x 1024 -> 3072: rotation, per-token int8, exact
+      int8 product, dequant + bias) in PyTorch on the CPU, 1 warm-up + median of 3;
+    - int8_oracle: the numpy oracle's int8-semantics forward of `n_images` image(s), one run (it restates the GPU
+      kernels' arithmetic, float64 BLAS for the exact int32 GEMMs).
+    The reference's own int8 path is CUDA and has no CPU counterpart."""
+    import numpy as np
+    import torch
+
+    from foidfinder_amd.engine import eva02_rope_tables
+    from oracle import float_torch as FT
     from oracle import model as OM
 
-    try:
-        from threadpoolctl import threadpool_info
-
-        threads = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
-    except Exception:  # noqa: BLE001
-        threads = os.cpu_count() or 1
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    cpu_raw = {k: v.detach().float().cpu() for k, v in raw.items()}
+    rope = eva02_rope_tables(cfg.grid, cfg.rope_ref)
+    fb = 2
+    imgs = torch.from_numpy(OM.synthetic_images(fb, cfg.img_size, seed=11)).float()
+    t_float = median_time(lambda: FT.forward_float(imgs, cpu_raw, cfg.depth, cfg.heads, cfg.patch, cfg.hidden, rope,
+                                                   cfg.eps))
+    x, qw, ws, b = OM.w8a8_linear_inputs()
+    xt, qwt, wst, bt = (torch.from_numpy(a) for a in (x, qw, ws, b))
+    t_lin = median_time(lambda: FT.w8a8_linear(xt, qwt, wst, bt))
+    lin_ops = 2 * x.shape[0] * qw.shape[0] * qw.shape[1]
     np_state = {k: v.detach().cpu().numpy() for k, v in state.items()}
     ocfg = OM.Eva02Config(img_size=cfg.img_size, depth=cfg.depth, tags=cfg.tags)
     images = OM.synthetic_images(n_images, cfg.img_size, seed=11)
     t = time.perf_counter()
     OM.forward_int8_state(images, np_state, ocfg)
-    dt = time.perf_counter() - t
-    return {"value": round(n_images / dt, 4), "unit": "images/s", "cores": threads, "kind": "port",
-            "sample": f"{n_images} image(s) through the full 24-block EVA02-L/14-448 int8 forward "
-                      f"(numpy oracle, float64 BLAS for the exact int32 GEMMs), {dt:.1f} s"}
+    t_int8 = time.perf_counter() - t
+    return {"value": round(fb / t_float, 4), "unit": "images/s", "cores": threads, "kind": "port",
+            "sample": f"EVA02-L/14-448 float forward, PyTorch fp32 on the CPU, batch {fb}, 1 warm-up + median of 3 "
+                      f"({t_float:.2f} s per batch)",
+            "torch_threads": torch.get_num_threads(), "cpu": cpu_info(),
+            "w8a8_linear": {"value": round(lin_ops / t_lin / 1e9, 2), "unit": "GOP/s", "ms": round(1e3 * t_lin, 2),
+                            "sample": "1025 x 1024 fp16 -> 3072, rotation + per-token int8 + exact int8 product + "
+                                      "dequant + bias, PyTorch CPU, 1 warm-up + median of 3"},
+            "int8_oracle": {"value": round(n_images / t_int8, 4), "unit": "images/s",
+                            "sample": f"{n_images} image(s) through the numpy int8-semantics forward, one run, "
+                                      f"{t_int8:.1f} s"}}
 
 
 def bench_pixai(args) -> None:
@@ -342,7 +403,6 @@ def main():
     t0 = time.perf_counter()
     raw = synthetic_checkpoint(cfg, seed=args.seed)
     state = convert_checkpoint({k: v.to(dev) for k, v in raw.items()}, cfg)
-    del raw
     eng = Eva02Int8(state, cfg, device=dev)
     g = torch.Generator(device="cpu").manual_seed(args.seed + 1)
     images = (torch.rand(B, cfg.img_size, cfg.img_size, 3, generator=g) * 2 - 1).half().to(dev)
@@ -384,7 +444,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(state, cfg, args.cpu_images)
+        cpu = cpu_baseline(raw, state, cfg, args.cpu_images)
     line = {
         "metric": METRIC,
         "value": round(ips, 2),

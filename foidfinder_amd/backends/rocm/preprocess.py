@@ -8,8 +8,8 @@ reference's PixAI preprocessing (foidfinder/backends/cuda/preprocess.py:16-32), 
 reference's tests/test_haruka.py:19-34): composited onto white, Pillow bicubic resize so the longer side is `size`,
 pasted centered on a white canvas, raw uint8 pixels NHWC (the normalization is folded into the patch weights). The
 resize runs on the GPU (`ff_resample_u8`, two separable passes with Pillow's fixed-point taps computed here) and is
-bit-exact with the installed Pillow's `Image.resize(BICUBIC)`, as the reference's Metal resize is
-(foidfinder/backends/mlx/kernels.py:75-186).
+bit-exact with Pillow 13's `Image.resize(BICUBIC)` (the version the reference pins), as the reference's Metal resize
+is (foidfinder/backends/mlx/kernels.py:75-186).
 """
 
 from __future__ import annotations
@@ -26,13 +26,12 @@ PILLOW_MAJOR = int(PIL.__version__.split(".")[0])
 
 
 def vertical_first(w: int, h: int, nw: int, nh: int) -> bool:
-    """Whether the installed Pillow resamples the height before the width (the passes do not commute: each rounds to
-    8 bits). Pillow 13, which the reference pins, does so when the height shrinks more than twice as much as the width
-    (the reference's resize_pad, foidfinder/backends/mlx/kernels.py:180-182); Pillow 12 when the source is more than
-    100 times as tall as it is wide (measured against Image.resize on both sides of the boundary)."""
-    if PILLOW_MAJOR >= 13:
-        return h - nh > 0 and h - nh > (w - nw) * 2
-    return h > 100 * w
+    """Whether the resize resamples the height before the width (the passes do not commute: each rounds to 8 bits).
+    Always the rule of Pillow 13, the version the reference pins (uv.lock) and hard-codes in its own resize: the
+    vertical pass first when the height shrinks more than twice as much as the width (the reference's resize_pad,
+    foidfinder/backends/mlx/kernels.py:180-182). So the served pixels do not depend on the Pillow installed here
+    (Pillow 12 orders the passes by another rule and differs in the last bit on tall images such as 448 x 900)."""
+    return h - nh > 0 and h - nh > (w - nw) * 2
 
 
 def rgb_on_white(image: Image.Image) -> Image.Image:

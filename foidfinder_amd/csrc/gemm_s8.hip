@@ -191,7 +191,7 @@ __device__ __forceinline__ void store_epilogue(const int16_t_v (&acc)[NI][MI], i
       if constexpr (EPI == FF_EPI_QKV_ROPE) {
         if (seg_rot) {
           const int L = args.rope_len;
-          const int tbytes = L * 32 * 4;  // rope_len <= 2^24 (checked on the host)
+          const int tbytes = buf_bytes(static_cast<int64_t>(L) * 32 * 4);  // rope_len < 2^24 (checked on the host)
 #pragma unroll
           for (int p = 0; p < 32 / ROWS_PER_PASS; ++p) {
             int r = rope_row0 + 32 * j + p * ROWS_PER_PASS;
@@ -1223,7 +1223,7 @@ extern "C" int ff_gemm_s8(const int8_t* A, const int8_t* W, int64_t M, int64_t N
   if (epi == FF_EPI_QKV_ROPE) {
     if (N % 3 != 0 || (N / 3) % 64 != 0) return fail(FF_EINVAL, "gemm_s8: QKV epilogue needs N = 3C with C % 64 == 0");
     if (!rope_cos || !rope_sin || rope_len <= 0) return fail(FF_EINVAL, "gemm_s8: QKV epilogue needs RoPE tables");
-    if (rope_len > (int64_t(1) << 24)) return fail(FF_EINVAL, "gemm_s8: rope_len > 2^24 is not supported");
+    if (rope_len >= (int64_t(1) << 24)) return fail(FF_EINVAL, "gemm_s8: rope_len >= 2^24 is not supported");
     if (!aligned(rope_cos, 16) || !aligned(rope_sin, 16)) return fail(FF_EINVAL, "gemm_s8: misaligned RoPE tables");
   }
   if (M == 0) return FF_OK;

@@ -21,6 +21,7 @@ import math
 from dataclasses import asdict, dataclass
 from pathlib import Path
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 
@@ -81,33 +82,57 @@ def hadamard(n: int, device: torch.device | str = "cpu") -> torch.Tensor:
 
 
 def quantize_rows_int8(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """Symmetric per-output-channel int8 in float32: w ~= q * scale[:, None] (engine.py:37-41)."""
+    """Symmetric per-output-channel int8 in float32: w ~= q * scale[:, None] (engine.py:37-41):
+    scale = max(amax, 1e-12) / 127 and q = clamp(round(w / scale), -127, 127), both divisions IEEE float32.
+
+    Each float32 quotient is formed as a float64 division of tensors rounded to float32, which is the correctly
+    rounded float32 quotient (double rounding is harmless for division when 53 >= 2 * 24 + 2) on every device:
+    torch's float32 division on the GPU is not always correctly rounded (a division by a scalar becomes a multiply
+    by its reciprocal), and a last-bit difference in a quotient near a rounding tie changes a code."""
     w = w.float()
-    scale = w.abs().amax(1).clamp_min(1e-12) / 127.0
-    q = torch.round(w / scale[:, None]).clamp(-127, 127).to(torch.int8)
+    amax = w.abs().amax(1).clamp_min(1e-12).double()
+    scale = (amax / torch.full_like(amax, 127.0)).float()
+    q = torch.round((w.double() / scale.double()[:, None]).float()).clamp(-127, 127).to(torch.int8)
     return q.contiguous(), scale.contiguous()
 
 
-def rotate_quantize(w: torch.Tensor, block: int) -> tuple[torch.Tensor, torch.Tensor]:
-    """quantize_rows_int8(W @ blockdiag(H_block)); the product in float64, rounded to float32 once."""
+def rotate_rows64(w: torch.Tensor, block: int) -> torch.Tensor:
+    """W [N, K] @ blockdiag(H_block) in float64 by a fast Walsh-Hadamard transform over each block of K columns:
+    butterflies (a, b) -> (a + b, a - b) over column bits 0, 1, 2, ... in that order, then x 1/sqrt(block). Every
+    step is one IEEE float64 operation in a fixed order, so the result is the same bits on the CPU and on the GPU
+    (a BLAS product sums in a device-dependent order and can differ in the last bit, which the rounding to float32
+    and the quantization below can turn into a different code)."""
     n, k = w.shape
-    h = hadamard(block, w.device)
-    wr = (w.double().reshape(n, k // block, block) @ h).reshape(n, k)
-    return quantize_rows_int8(wr.float())
+    v = w.double().reshape(n, k // block, block)
+    half = 1
+    while half < block:
+        v = v.reshape(n, k // block, block // (2 * half), 2, half)
+        a, b = v[..., 0, :], v[..., 1, :]
+        v = torch.stack((a + b, a - b), dim=-2)
+        half *= 2
+    return v.reshape(n, k) * (1.0 / math.sqrt(block))
+
+
+def rotate_quantize(w: torch.Tensor, block: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """quantize_rows_int8(W @ blockdiag(H_block)); the product in float64 (rotate_rows64), rounded to float32 once
+    (the reference forms it in fp32 with cuBLAS, engine.py:59)."""
+    return quantize_rows_int8(rotate_rows64(w, block).float())
 
 
 def eva02_rope_tables(grid: int, ref: int, head_dim: int = 64) -> tuple[torch.Tensor, torch.Tensor]:
     """EVA02 axial RoPE per interleaved pair: cos/sin fp32 [1 + grid^2, head_dim/2]; row 0 (cls) is the identity;
-    pairs 0..15 take the row position, 16..31 the column position, rescaled to the pretraining grid
-    (foidfinder/backends/mlx/haruka.py:22-33)."""
+    pairs 0..15 take the row position, 16..31 the column position, rescaled to the pretraining grid. Computed as the
+    reference computes its tables, in float32 numpy arithmetic throughout (bands, positions, angles, cos and sin;
+    foidfinder/backends/mlx/haruka.py:22-33), so the served tables carry the reference's roundings."""
     q = head_dim // 4
-    bands = 1.0 / (10000.0 ** (torch.arange(q, dtype=torch.float64) / q))
-    t = torch.arange(grid, dtype=torch.float64) / grid * ref
-    ty, tx = torch.meshgrid(t, t, indexing="ij")
-    ang = torch.cat([ty.reshape(-1, 1) * bands, tx.reshape(-1, 1) * bands], dim=1)  # float64, rounded once below
-    cos = torch.cat([torch.ones(1, head_dim // 2, dtype=torch.float64), torch.cos(ang)]).float()
-    sin = torch.cat([torch.zeros(1, head_dim // 2, dtype=torch.float64), torch.sin(ang)]).float()
-    return cos.contiguous(), sin.contiguous()
+    bands = np.float32(1.0) / (np.float32(10000.0) ** (np.arange(q, dtype=np.float32) / np.float32(q)))
+    t = np.arange(grid, dtype=np.float32) / np.float32(grid) * np.float32(ref)
+    ty, tx = np.meshgrid(t, t, indexing="ij")
+    ang = np.concatenate([ty.reshape(-1, 1) * bands, tx.reshape(-1, 1) * bands], axis=1)
+    cos = np.concatenate([np.ones((1, head_dim // 2), np.float32), np.cos(ang)])
+    sin = np.concatenate([np.zeros((1, head_dim // 2), np.float32), np.sin(ang)])
+    assert cos.dtype == np.float32 and sin.dtype == np.float32
+    return torch.from_numpy(np.ascontiguousarray(cos)), torch.from_numpy(np.ascontiguousarray(sin))
 
 
 def convert_checkpoint(raw: dict[str, torch.Tensor], cfg: Eva02Config) -> dict[str, torch.Tensor]:

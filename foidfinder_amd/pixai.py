@@ -299,6 +299,34 @@ class PixAIInt8(Int8Engine):
         return self.pool_head(x.view(B, L, d))
 
 
+def write_int8_dir(model_dir: str | Path, output: str | Path, device: str | torch.device | None = None) -> Path:
+    """Writes the reference's converted PixAI checkpoint (the output of `foidfinder convert`, cli.py:143-161) from an
+    official model directory: `model.safetensors` with each block linear as `<name>.qweight` int8 [N, K],
+    `<name>.wscale` fp32 [N] and `<name>.bias` fp32 [N] (every other tensor copied unchanged) and the metadata
+    `{"format": "foidfinder-pixai-int8-v1"}` (engine.py:44-62), plus the source's `config.json`. The conversion runs
+    on `device` (the GPU when present, as the reference's does) and is the same bits on any device. Returns the
+    output directory; `load_pixai_dir` and the reference's loader (engine.py:68-70) read it without converting."""
+    import shutil
+
+    from safetensors.torch import load_file, save_file
+
+    model_dir, output = Path(model_dir), Path(output)
+    if device is None:
+        device = "cuda" if torch.cuda.is_available() else "cpu"
+    state = load_file(str(model_dir / "model.safetensors"), device=str(device))
+    if "blocks.0.attn.qkv.qweight" in state:
+        raise RuntimeError(f"{model_dir}: already in the int8 format")
+    config = json.loads((model_dir / "config.json").read_text())
+    over = dict(config.get("foidfinder_rocm", {}))
+    if "global_blocks" in over:
+        over["global_blocks"] = tuple(over["global_blocks"])
+    out = convert_checkpoint(state, config_from_state(state, **over))
+    output.mkdir(parents=True, exist_ok=True)
+    save_file({k: v.contiguous().cpu() for k, v in out.items()}, str(output / "model.safetensors"), {"format": FORMAT})
+    shutil.copy(model_dir / "config.json", output / "config.json")
+    return output
+
+
 def load_pixai_dir(model_dir: str | Path, device: str | torch.device = "cuda") -> tuple[PixAIInt8, dict]:
     """A PixAI model directory as the reference reads it (config.json + model.safetensors, official fp32 weights or
     the converted int8 format; engine.py:65-72). Dimensions come from the weights; an optional

@@ -24,6 +24,10 @@ runs those checks.
 PINNED = {
     "model.hadamard": "closed form (-1)^popcount(i&j)/sqrt(n), H H = I, H e0 = 1/sqrt(n)",
     "model.quantize_rows_int8": "brute-force per-element search of the nearest code on small matrices; ties",
+    "model.rotate_rows64": "equals W @ blockdiag(H) formed as a float64 product, to float64 rounding (blocks 1024 and "
+    "128); a planted wrong-sign butterfly fails it",
+    "model.eva02_rope_tables": "cls row identity; every entry within 4e-6 of cos/sin of float64 angles (a planted "
+    "row/column swap fails); one entry recomputed step by step in the reference's float32 recipe",
     "rotq8.fwht_rows": "equals x @ H (float64) to fp32 rounding; stage order only changes rounding (Parseval)",
     "rotq8.rot_q8_1024": "dequantized codes reconstruct x @ H within half a code; zero row, one-hot row, "
     "RNE ties; LayerNorm variant vs float64 LayerNorm",

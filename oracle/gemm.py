@@ -41,11 +41,28 @@ def fma32(a: np.ndarray, b: np.ndarray, c: np.ndarray) -> np.ndarray:
 
     a * b is exact in float64 (24 + 24 significant bits); Knuth's TwoSum splits p + c exactly into s + e in float64.
     Rounding s to float32 is then the correct rounding of p + c unless s lies exactly halfway between two float32
-    values and e != 0: the sign of e then decides (numpy's tie-to-even would ignore it)."""
+    values and e != 0: the sign of e then decides (numpy's tie-to-even would ignore it). (No float32 midpoint can lie
+    strictly between p + c and s, since it would be a float64 value nearer to p + c than s.)
+
+    The midpoint test runs on the float64 bits: in float32's normal range a float32 midpoint has exactly bit 28 set
+    among the 29 low fraction bits that float32 drops. Only such elements, and those outside the normal range
+    (subnormal, overflowing, non-finite), take the TwoSum path."""
     a, b, c = np.broadcast_arrays(np.asarray(a, F32), np.asarray(b, F32), np.asarray(c, F32))
     p = a.astype(np.float64) * b.astype(np.float64)
     c64 = c.astype(np.float64)
     s = p + c64
+    r = s.astype(F32)
+    mag = np.abs(s)
+    cand = ((s.view(np.int64) & ((1 << 29) - 1)) == (1 << 28)) | ~(mag >= 2.0**-125) | (mag >= 2.0**127)
+    if not cand.any():
+        return r
+    idx = np.nonzero(cand)
+    r[idx] = _fma32_twosum(p[idx], c64[idx], s[idx])
+    return r
+
+
+def _fma32_twosum(p: np.ndarray, c64: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """fma32's exact path on 1-D float64 operands: p = a * b exact, s = p + c rounded to float64."""
     bb = s - p
     e = (p - (s - bb)) + (c64 - bb)
     r = s.astype(F32)

@@ -52,29 +52,40 @@ def quantize_rows_int8(w: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     return np.ascontiguousarray(q), scale.astype(F32)
 
 
+def rotate_rows64(w: np.ndarray, block: int) -> np.ndarray:
+    """W [N, K] @ blockdiag(H_block) in float64 as a fast Walsh-Hadamard transform per block of K columns: butterflies
+    (a, b) -> (a + b, a - b) over column bits 0, 1, 2, ... in that order, then x 1/sqrt(block); each step one IEEE
+    float64 operation, so the bits do not depend on a BLAS summation order."""
+    n, k = w.shape
+    v = w.astype(np.float64).reshape(n, k // block, block)
+    half = 1
+    while half < block:
+        v = v.reshape(n, k // block, block // (2 * half), 2, half)
+        v = np.stack((v[..., 0, :] + v[..., 1, :], v[..., 0, :] - v[..., 1, :]), axis=-2)
+        half *= 2
+    return v.reshape(n, k) * (1.0 / math.sqrt(block))
+
+
 def rotate_quantize(w: np.ndarray, block: int) -> tuple[np.ndarray, np.ndarray]:
-    """W [N, K] -> quantize_rows_int8(W @ blockdiag(H_block)); the product in float64, rounded to float32 once
-    (the reference multiplies in float32, engine.py:59; float64 makes the synthetic weights platform-independent)."""
-    k = w.shape[1]
-    if block == k:
-        wr = w.astype(np.float64) @ hadamard(k)
-    else:  # apply per 128-column block without forming the big matrix
-        h = hadamard(block)
-        wr = (w.astype(np.float64).reshape(w.shape[0], k // block, block) @ h).reshape(w.shape)
-    return quantize_rows_int8(wr.astype(F32))
+    """W [N, K] -> quantize_rows_int8(W @ blockdiag(H_block)); the product in float64 (rotate_rows64), rounded to
+    float32 once (the reference multiplies in float32, engine.py:59; float64 makes the codes platform-independent)."""
+    return quantize_rows_int8(rotate_rows64(w, block).astype(F32))
 
 
 def eva02_rope_tables(grid: int, ref: int, head_dim: int = 64) -> tuple[np.ndarray, np.ndarray]:
     """EVA02 axial RoPE as consumed by the QKV epilogue: cos/sin fp32 [1 + grid^2, head_dim/2], one entry per
     interleaved (even, odd) pair; row 0 (cls) is the identity. Angles: pairs 0..15 use the row (y) position, pairs
-    16..31 the column (x) position, positions rescaled to the pretraining grid (foidfinder/backends/mlx/haruka.py:22-33)."""
+    16..31 the column (x) position, positions rescaled to the pretraining grid. Every step in float32, as the
+    reference's recipe (foidfinder/backends/mlx/haruka.py:22-33: float32 bands and positions, float32 products,
+    numpy's float32 cos and sin; its tables repeat each pair's angle twice, kept here once per pair)."""
     q = head_dim // 4
-    bands = 1.0 / (10000.0 ** (np.arange(q, dtype=np.float64) / q))
-    t = np.arange(grid, dtype=np.float64) / grid * ref
+    bands = F32(1.0) / (F32(10000.0) ** (np.arange(q, dtype=F32) / F32(q)))
+    t = np.arange(grid, dtype=F32) / F32(grid) * F32(ref)
     ty, tx = np.meshgrid(t, t, indexing="ij")
-    ang = np.concatenate([ty.reshape(-1, 1) * bands, tx.reshape(-1, 1) * bands], axis=1)  # float64, rounded once
-    cos = np.concatenate([np.ones((1, head_dim // 2)), np.cos(ang)]).astype(F32)
-    sin = np.concatenate([np.zeros((1, head_dim // 2)), np.sin(ang)]).astype(F32)
+    ang = np.concatenate([ty.reshape(-1, 1) * bands, tx.reshape(-1, 1) * bands], axis=1)
+    cos = np.concatenate([np.ones((1, head_dim // 2), F32), np.cos(ang)])
+    sin = np.concatenate([np.zeros((1, head_dim // 2), F32), np.sin(ang)])
+    assert cos.dtype == F32 and sin.dtype == F32
     return np.ascontiguousarray(cos), np.ascontiguousarray(sin)
 
 
@@ -232,13 +243,17 @@ def layer_norm(x: np.ndarray, g: np.ndarray, b: np.ndarray, eps: float) -> np.nd
     return (x - mu) / np.sqrt(var + eps) * g + b
 
 
-def head(x: np.ndarray, w: FloatWeights) -> np.ndarray:
-    """Final LayerNorm on the cls token, tag head GEMM, sigmoid -> float32 probabilities [B, tags]."""
+def head_logits(x: np.ndarray, w: FloatWeights) -> np.ndarray:
+    """Final LayerNorm on the cls token and the tag head GEMM, float64 -> logits [B, tags]."""
     cfg = w.cfg
     cls = x.reshape(-1, cfg.tokens, cfg.dim)[:, 0]
     h = layer_norm(cls, w.norm_w, w.norm_b, cfg.eps)
-    logits = h @ w.head_w.T.astype(np.float64) + w.head_b
-    return (1.0 / (1.0 + np.exp(-logits))).astype(F32)
+    return h @ w.head_w.T.astype(np.float64) + w.head_b
+
+
+def head(x: np.ndarray, w: FloatWeights) -> np.ndarray:
+    """head_logits then the sigmoid -> float32 probabilities [B, tags]."""
+    return (1.0 / (1.0 + np.exp(-head_logits(x, w)))).astype(F32)
 
 
 def block_int8(
@@ -277,18 +292,29 @@ def block_int8(
     return G.gemm_s8(h8, qb["fc2.qweight"], rs, qb["fc2.wscale"], qb["fc2.bias"], G.EPI_RESIDUAL, residual=x)
 
 
-def forward_int8(images: np.ndarray, w: FloatWeights, qblocks: list[dict[str, np.ndarray]]) -> np.ndarray:
-    """images [B, S, S, 3] -> probabilities [B, tags] with the int8 engine's semantics."""
+def forward_int8_x(images: np.ndarray, w: FloatWeights, qblocks: list[dict[str, np.ndarray]]) -> np.ndarray:
+    """images [B, S, S, 3] -> the fp16 residual stream [B*L, d] after the last block, with the int8 engine's
+    semantics."""
     cfg = w.cfg
     rope = eva02_rope_tables(cfg.grid, cfg.rope_ref)
     x = stem(images, w)
     for qb in qblocks:
         x = block_int8(x, qb, cfg, rope)
-    return head(x, w)
+    return x
+
+
+def forward_int8(images: np.ndarray, w: FloatWeights, qblocks: list[dict[str, np.ndarray]]) -> np.ndarray:
+    """images [B, S, S, 3] -> probabilities [B, tags] with the int8 engine's semantics."""
+    return head(forward_int8_x(images, w, qblocks), w)
 
 
 def forward_float(images: np.ndarray, w: FloatWeights) -> np.ndarray:
     """The same model without quantization, float64 throughout (the float reference the int8 path approximates)."""
+    return head(forward_float_x(images, w), w)
+
+
+def forward_float_x(images: np.ndarray, w: FloatWeights) -> np.ndarray:
+    """forward_float's residual stream [B*L, d] after the last block, float64."""
     cfg = w.cfg
     cos, sin = eva02_rope_tables(cfg.grid, cfg.rope_ref)
     B, L, d, H = images.shape[0], cfg.tokens, cfg.dim, cfg.heads
@@ -316,7 +342,7 @@ def forward_float(images: np.ndarray, w: FloatWeights) -> np.ndarray:
         g, val = gx[:, : cfg.hidden], gx[:, cfg.hidden :]
         h = layer_norm(g / (1.0 + np.exp(-g)) * val, blk["mlp_norm_w"], blk["mlp_norm_b"], cfg.eps)
         x = x + h @ blk["fc2_w"].T.astype(np.float64) + blk["fc2_b"]
-    return head(x, w)
+    return x
 
 
 def synthetic_images(batch: int, size: int, seed: int = 1) -> np.ndarray:

@@ -102,3 +102,50 @@ def letterbox(rgb: np.ndarray, size: int, pillow_major: int = 12) -> np.ndarray:
     tmp = resample_pass(rgb, 0, kh, bh, (rows, nw), (0, 0, rows, nw), row0)
     bv = bv - np.array([row0, 0], np.int32)
     return resample_pass(tmp, 1, kv, bv, (size, size), (top, left, nh, nw))
+
+
+def bilinear_aa_matrix(in_size: int, out_size: int) -> np.ndarray:
+    """Antialiased bilinear resampling along one axis as a float64 [out_size, in_size] matrix: what PixAI's
+    preprocessing (torchvision's resize, i.e. torch's interpolate(mode="bilinear", antialias=True,
+    align_corners=False); foidfinder/backends/cuda/preprocess.py:27-28) computes.
+
+    scale = in / out. Output i is centered at input coordinate (i + 0.5) * scale; the filter is the triangle
+    max(0, 1 - |t|) with t = (j + 0.5 - center) / max(scale, 1), i.e. stretched over the downscale factor so that
+    every input pixel contributes (plain bilinear when enlarging). The taps are the input indices j in
+    [trunc(center - support + 0.5), trunc(center + support + 0.5)) clipped to the input, support = max(scale, 1), and
+    their weights are divided by their sum (so rows at the borders renormalize instead of reading past the edge)."""
+    scale = in_size / out_size
+    stretch = max(scale, 1.0)
+    out = np.zeros((out_size, in_size), np.float64)
+    for i in range(out_size):
+        center = (i + 0.5) * scale
+        lo = max(int(center - stretch + 0.5), 0)
+        hi = min(int(center + stretch + 0.5), in_size)
+        j = np.arange(lo, hi)
+        w = np.maximum(0.0, 1.0 - np.abs((j + 0.5 - center) / stretch))
+        if w.sum() > 0:
+            out[i, lo:hi] = w / w.sum()
+    return out
+
+
+def resize_2d(x: np.ndarray, rows: np.ndarray, cols: np.ndarray) -> np.ndarray:
+    """x [H, W, C] -> rows @ x @ cols^T per channel: [nh, nw, C] (separable resampling, float64)."""
+    t = np.tensordot(rows, x, axes=(1, 0))  # [nh, W, C]
+    return np.tensordot(t, cols, axes=(1, 1)).transpose(0, 2, 1)  # [nh, C, nw] -> [nh, nw, C]
+
+
+def letterbox_pixai(rgb: np.ndarray, size: int) -> np.ndarray:
+    """PixAI's letterbox (foidfinder/backends/cuda/preprocess.py:16-32) in float64: uint8 RGB [H, W, 3] scaled to
+    [0, 1], resized with the antialiased bilinear filter so the longer side is `size` (the other side int(side * r),
+    r = min(size / H, size / W); no resize when that leaves the size unchanged), normalized to [-1, 1] and centered on
+    a canvas of -1 at offsets ((size - nh) // 2, (size - nw) // 2). Returns float64 [size, size, 3]."""
+    h, w = rgb.shape[:2]
+    x = rgb.astype(np.float64) / 255.0
+    r = min(size / h, size / w)
+    nh, nw = int(h * r), int(w * r)
+    if (nh, nw) != (h, w):
+        x = resize_2d(x, bilinear_aa_matrix(h, nh), bilinear_aa_matrix(w, nw))
+    out = np.full((size, size, 3), -1.0)
+    top, left = (size - nh) // 2, (size - nw) // 2
+    out[top : top + nh, left : left + nw] = x * 2.0 - 1.0
+    return out

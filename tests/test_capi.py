@@ -75,6 +75,8 @@ def test_gemm_s8_rejects_bad_arguments():
     assert "variant" in call(variant=99)[1]
     assert "QKV" in call(N=48, epi=0)[1]  # N = 3C needs C % 64 == 0
     assert "RoPE" in call(N=192, epi=0)[1]
+    assert "rope_len" in call(N=192, epi=0, rope=(256, 256, 1 << 24))[1]  # table bytes must fit 31 bits
+    assert "rope_len" not in call(N=192, epi=0, rope=(256, 256, (1 << 24) - 1), ptrs=8)[1]  # largest accepted
     assert call(M=0) == (FF_OK, "")
     assert "misaligned" in call(ptrs=8)[1]
     assert "not supported" in call(Kd=(1 << 22) + 64)[1]  # 32-bit offsets within a tile

@@ -1,6 +1,6 @@
 """The EVA02 int8 engine on the GPU against the CPU oracle, same converted weights.
 
-Why three bars. Every block kernel is bit-exact with the oracle on identical inputs (tests/test_kernels_gpu.py),
+Why these bars. Every block kernel is bit-exact with the oracle on identical inputs (tests/test_kernels_gpu.py),
 except attention, whose fp32 MFMA sums cannot be restated bit for bit on the CPU. Attention mixes all tokens, and
 every rotate+quant downstream turns a last-bit change into occasional one-step code flips. So a single ulp of
 difference grows, within a block or two, to the size of the int8 quantization noise itself (the oracle's own int8
@@ -9,8 +9,11 @@ forward differs from the unquantized float forward by the same amount). Hence:
   1. wiring, bit-exact: the oracle takes the engine's stem output and per-block attention outputs (teacher forcing)
      and must reproduce every qkv and every block output bit for bit;
   2. attention per block: within 4e-3 absolute of float64 attention on the engine's own qkv;
-  3. end to end: |p_engine - p_oracle_int8| within 1.5x the int8 noise budget |p_oracle_int8 - p_float|
-     (max and mean over tags and images), with the logits finite.
+  3. end to end on a small model (2 blocks, 112 px): |p_engine - p_oracle_int8| within 1.5x the int8 noise budget
+     |p_oracle_int8 - p_float| (max and mean over tags and images), with the logits finite;
+  4. end to end at the benchmark's model (24 blocks, 1025 tokens) against stated absolute bars (E2E_BARS and
+     E2E_RMS_REL_X): max and mean |dp|, max |dlogit|, the reference's decision-stability rule, the same top-1 tag and
+     gap-filtered top-k, against both the int8 oracle and the float forward.
 """
 
 from __future__ import annotations
@@ -167,3 +170,119 @@ def test_full_size_batch_32_is_permutation_equivariant(dev):
     shuffled = eng(images[perm].contiguous()).clone()
     torch.cuda.synchronize()
     assert torch.equal(shuffled, full[perm]), "permuting the batch does not permute the logits"
+
+
+# The stated end-to-end bar at the benchmark's model (EVA02-L/14-448, 24 blocks, 1025 tokens), without teacher
+# forcing, against each reference: (max |dp|, mean |dp|, max |dlogit|) over all tags of both images. Reasoning and
+# measurements are in the docstring of the test.
+E2E_BARS = {"int8 oracle": (0.15, 0.005, 0.8), "float": (0.15, 0.005, 1.0)}
+E2E_RMS_REL_X = 0.12  # rms(x_engine - x_oracle) / rms(x_oracle) for the residual stream after the last block
+
+
+def decision_flips(p, p_ref):
+    """The reference's decision-stability rule (tests/test_cuda_engine.py:55-57): a tag the reference scores above
+    0.65 must stay above 0.5, one below 0.35 must stay below 0.5. Returns the number of violations."""
+    return int(((p_ref > 0.65) & (p <= 0.5)).sum() + ((p_ref < 0.35) & (p >= 0.5)).sum())
+
+
+def gap_filtered_topk(logits, ref, kmax=50):
+    """Per image, every k <= kmax whose reference logit gap between rank k and rank k + 1 exceeds twice that image's
+    largest logit error: the engine's top-k set must be the reference's. Returns (checked k count, mismatches)."""
+    checked, bad = 0, []
+    for i in range(ref.shape[0]):
+        err = np.abs(logits[i] - ref[i]).max()
+        order = np.argsort(-ref[i])
+        srt = ref[i][order]
+        mine = np.argsort(-logits[i])
+        for k in range(1, kmax + 1):
+            if srt[k - 1] - srt[k] > 2 * err:
+                checked += 1
+                if set(mine[:k]) != set(order[:k]):
+                    bad.append((i, k))
+    return checked, bad
+
+
+@pytest.mark.timeout(900)
+def test_full_depth_eva02_l_end_to_end(dev):
+    """EVA02-L/14-448 (24 blocks, 1025 tokens) on 2 seeded images through the served path (graph replay), against the
+    int8 oracle forward and against the float64 forward of the same weights, with no teacher forcing.
+
+    Why these bars. Every block kernel is bit-exact with the oracle on identical inputs except attention (fp32 MFMA
+    sums, hardware exp2, p rounded to fp16 for the PV product), whose fp16 outputs differ from float64 attention by a
+    few ulps. The next rotate+quant maps values of ~38 code steps to codes, so a relative change of ~1e-3 moves a few
+    percent of the codes by one step; such flips recur in every block, and the engine and the int8 oracle drift apart
+    like two int8 models with independent rounding. Measured at this seed: rms relative difference of the residual
+    stream 1.2 % after block 1 and 8.2 % after block 24, against 2.0 % and 10.0 % between the int8 oracle and the
+    float forward (the int8 noise itself); logits differ by up to ~0.6 (engine vs int8 oracle) and ~0.75 (vs float),
+    with head weights N(0, 0.05) over LayerNorm outputs (logit spread 1.6). Sigmoid outputs therefore cannot agree to
+    2e-3. The bars: the reference's own for its int8 engine against the fp32 model, max |dp| < 0.15
+    (tests/test_cuda_engine.py:54), against both references (measured 0.122 and 0.133); mean |dp| <= 0.005
+    (measured 0.0022 and 0.0026; the reference's 1e-4 is for its real checkpoint, where nearly every tag sits at
+    p ~ 0) and max |dlogit| as in E2E_BARS; the reference's decision-stability rule
+    (tests/test_cuda_engine.py:55-57) with no violation; the same top-1 tag; and identical
+    top-k for every k <= 50 where the reference's logit gap between ranks k and k + 1 exceeds twice the image's
+    largest logit error (checked for at least one k). The head's bias is spread like a trained tagger's output:
+    N(-6, 2^2) for most tags (confidently absent, with a tail near 0.5 for the decision rule) and 12 confident tags
+    2.5 logits apart, so that ties do not decide the top-k."""
+    from foidfinder_amd.engine import Eva02Config, Eva02Int8, convert_checkpoint, synthetic_checkpoint
+
+    cfg = Eva02Config()
+    raw = synthetic_checkpoint(cfg, seed=3)
+    g = torch.Generator().manual_seed(11)
+    bias = -6.0 + 2.0 * torch.randn(cfg.tags, generator=g)  # most tags confidently absent, a tail near 0.5
+    present = torch.randperm(cfg.tags, generator=g)[:12]
+    bias[present] = 4.0 + 2.5 * torch.arange(12, dtype=torch.float32)  # a few confident tags, 2.5 logits apart
+    raw["head.bias"] = bias
+    state = convert_checkpoint(raw, cfg)
+    eng = Eva02Int8(state, cfg, device=dev)
+    images = OM.synthetic_images(2, cfg.img_size, seed=8)
+    print("full-depth end to end: engine forward (graph, batch 2)", flush=True)
+    served = eng(torch.from_numpy(images).to(dev)).cpu().numpy().astype(np.float64)
+    trace = {}
+    eager = eng.eager(torch.from_numpy(images).to(dev), trace).cpu().numpy().astype(np.float64)
+    assert np.array_equal(served, eager), "graph replay differs from the eager forward"
+    x_eng = trace[f"x{cfg.depth - 1}"].cpu().numpy()
+
+    np_state = {k: v.numpy() for k, v in state.items()}
+    ocfg = oracle_cfg(cfg)
+    fw = OM.float_weights_from_state(np_state, ocfg)
+    qblocks = OM.blocks_from_state(np_state, cfg.depth)
+    fweights = float_weights(raw, ocfg)
+    from concurrent.futures import ThreadPoolExecutor
+
+    def job(arg):
+        kind, i = arg
+        one = images[i : i + 1]
+        return OM.forward_int8_x(one, fw, qblocks) if kind == "int8" else OM.forward_float_x(one, fweights)
+
+    print("full-depth end to end: oracle int8 and float64 forwards", flush=True)
+    with ThreadPoolExecutor(4) as ex:
+        xs = list(ex.map(job, [("int8", 0), ("int8", 1), ("float", 0), ("float", 1)]))
+    x_int8, x_float = np.concatenate(xs[:2]), np.concatenate(xs[2:])
+    ref_int8, ref_float = OM.head_logits(x_int8, fw), OM.head_logits(x_float, fweights)
+
+    rms = lambda d, r: float(np.sqrt((d.astype(np.float64) ** 2).mean() / (r.astype(np.float64) ** 2).mean()))
+    drift = rms(x_eng.astype(np.float64) - x_int8, x_int8)
+    noise = rms(x_int8.astype(np.float64) - x_float, x_float)
+    sig = lambda z: 1.0 / (1.0 + np.exp(-z))
+    p = sig(served)
+    report = [f"residual stream after block 24: engine vs int8 oracle rms rel {drift:.4f}, "
+              f"int8 oracle vs float {noise:.4f}"]
+    for name, ref in (("int8 oracle", ref_int8), ("float", ref_float)):
+        dp, dl = np.abs(p - sig(ref)), np.abs(served - ref)
+        checked, bad = gap_filtered_topk(served, ref)
+        report.append(f"vs {name}: max|dp| {dp.max():.4f} mean {dp.mean():.5f}; max|dlogit| {dl.max():.4f} "
+                      f"mean {dl.mean():.4f}; decision flips {decision_flips(p, sig(ref))}; top-1 "
+                      f"{[int(np.argmax(served[i]) == np.argmax(ref[i])) for i in range(2)]}; gap-filtered top-k "
+                      f"checked {checked}, mismatched {bad}")
+    print("\n".join(report), flush=True)
+    assert drift <= E2E_RMS_REL_X, report[0]
+    for name, ref in (("int8 oracle", ref_int8), ("float", ref_float)):
+        max_dp, mean_dp, max_dl = E2E_BARS[name]
+        dp, dl = np.abs(p - sig(ref)), np.abs(served - ref)
+        assert dp.max() <= max_dp and dp.mean() <= mean_dp, report
+        assert dl.max() <= max_dl, report
+        assert decision_flips(p, sig(ref)) == 0, report
+        assert all(np.argmax(served[i]) == np.argmax(ref[i]) for i in range(2)), report
+        checked, bad = gap_filtered_topk(served, ref)
+        assert checked > 0 and not bad, report

@@ -254,7 +254,7 @@ def test_pass_order_rules():
     for w, h in RESIZE_CASES:
         r = min(448 / w, 448 / h)
         nw, nh = max(1, int(w * r)), max(1, int(h * r))
-        assert P.vertical_first(w, h, nw, nh) == ORS.vertical_first(w, h, nw, nh, P.PILLOW_MAJOR)
+        assert P.vertical_first(w, h, nw, nh) == ORS.vertical_first(w, h, nw, nh, 13)  # the served rule: Pillow 13
     # the reference's rule for Pillow 13 (its resize_pad): (448, 900) shrinks the height over twice as much
     assert ORS.vertical_first(448, 900, 223, 448, 13) and not ORS.vertical_first(850, 1200, 317, 448, 13)
 

@@ -219,26 +219,30 @@ RESIZE_CASES = [(850, 1200), (448, 900), (3, 5000), (5000, 3), (100, 37), (448, 
 
 @pytest.mark.parametrize(("w", "h"), RESIZE_CASES)
 def test_gpu_letterbox_is_bit_exact_with_pillow(dev, w, h):
-    """The Haruka letterbox on the GPU (ff_resample_u8, two passes) against Pillow's own Image.resize(BICUBIC)
-    pasted on white: the reference's cases (tests/test_haruka.py:36-55), both sides of the installed Pillow's
-    pass-order boundary, and an image already at the input size."""
+    """The Haruka letterbox on the GPU (ff_resample_u8, two passes) against the oracle's letterbox in the pass order of
+    Pillow 13, the version the reference pins: the reference's cases (tests/test_haruka.py:36-55), both sides of the
+    pass-order boundaries, and an image already at the input size. Where the installed Pillow orders the passes the
+    same way, also against Pillow's own Image.resize(BICUBIC) pasted on white (the oracle's passes are pinned against
+    Pillow in both orders by the CPU tests)."""
     from PIL import Image
 
-    from foidfinder_amd.backends.rocm.preprocess import letterbox_gpu
+    from foidfinder_amd.backends.rocm.preprocess import PILLOW_MAJOR, letterbox_gpu
+    from oracle import resample as ORS
 
     s = 448
     rgb = np.random.default_rng(w * h).integers(0, 256, (h, w, 3), dtype=np.uint8)
     out = torch.full((s, s, 3), 7, dtype=torch.uint8, device=dev)
     letterbox_gpu(rgb, s, out)
+    got = out.cpu().numpy()
+    assert np.array_equal(got, ORS.letterbox(rgb, s, 13))
+    r = min(s / w, s / h)
+    nw, nh = max(1, int(w * r)), max(1, int(h * r))
     if (w, h) == (s, s):
-        want = rgb
-    else:
-        r = min(s / w, s / h)
-        nw, nh = max(1, int(w * r)), max(1, int(h * r))
+        assert np.array_equal(got, rgb)
+    elif ORS.vertical_first(w, h, nw, nh, 13) == ORS.vertical_first(w, h, nw, nh, PILLOW_MAJOR):
         canvas = Image.new("RGB", (s, s), (255, 255, 255))
         canvas.paste(Image.fromarray(rgb).resize((nw, nh), Image.Resampling.BICUBIC), ((s - nw) // 2, (s - nh) // 2))
-        want = np.asarray(canvas)
-    assert np.array_equal(out.cpu().numpy(), want)
+        assert np.array_equal(got, np.asarray(canvas))
 
 
 def test_preprocess_haruka_batch(dev):
@@ -258,3 +262,35 @@ def test_preprocess_haruka_batch(dev):
         one = torch.empty(112, 112, 3, dtype=torch.uint8, device=dev)
         letterbox_gpu(np.asarray(im), 112, one)
         assert torch.equal(out[i], one)
+
+
+@pytest.mark.timeout(600)
+def test_haruka_config5_full_shape(dev):
+    """Haruka at the benchmark's shape: EVA02-B/14-448, 12 blocks, tree pool, 98 782 tags, batch 64 of raw pixels
+    (the reference's model, foidfinder/haruka.py:13-27). Properties that hold at any size: finite logits; the graph
+    replay equals the eager forward bit for bit; permuting the batch permutes the logits bit for bit (blocks work per
+    token or per sequence, and the pool and head GEMMs see the same shapes). And the pool head plus the 98 782-column
+    head, on the engine's own final stream of one image, within 3e-3 in probability of the oracle's float64 head."""
+    from foidfinder_amd.haruka import HarukaConfig, HarukaInt8, convert_checkpoint, synthetic_checkpoint
+
+    cfg, ocfg = HarukaConfig(), OH.HarukaConfig()
+    state = convert_checkpoint(synthetic_checkpoint(cfg, seed=12), cfg)
+    eng = HarukaInt8(state, cfg, device=dev)
+    img = torch.from_numpy(pixels(64, cfg, seed=13)).to(dev)
+    print("haruka batch 64: graph", flush=True)
+    full = eng(img).clone()
+    torch.cuda.synchronize()
+    assert full.shape == (64, 98782) and torch.isfinite(full).all()
+    print("haruka batch 64: eager with trace", flush=True)
+    trace = {}
+    assert torch.equal(eng.eager(img, trace), full), "graph replay differs from eager at batch 64"
+    perm = torch.randperm(64, generator=torch.Generator().manual_seed(1)).to(dev)
+    shuffled = eng(img[perm].contiguous()).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(shuffled, full[perm]), "permuting the batch does not permute the logits"
+    x0 = trace[f"x{cfg.depth - 1}"][: cfg.tokens].cpu().numpy()
+    del trace
+    st = {k: v.numpy() for k, v in state.items() if not k.startswith("blocks.")}
+    want = OH.head(x0, st, ocfg)[0]
+    p, pw = 1 / (1 + np.exp(-full[0].double().cpu().numpy())), 1 / (1 + np.exp(-want))
+    assert np.abs(p - pw).max() < 3e-3, f"pool head + head off by {np.abs(p - pw).max()}"

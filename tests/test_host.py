@@ -53,6 +53,12 @@ def test_convert_checkpoint_matches_oracle_conversion():
                 np.testing.assert_array_equal(conv[p + long + "." + f].numpy(), want[f"{short}.{f}"], err_msg=long + f)
 
 
+def test_weight_rotation_matches_oracle_bit_for_bit(rng):
+    for block, k in ((1024, 1024), (128, 2816)):
+        w = (rng.standard_normal((40, k)) * 0.02).astype(np.float32)
+        np.testing.assert_array_equal(E.rotate_rows64(torch.from_numpy(w), block).numpy(), OM.rotate_rows64(w, block))
+
+
 def test_rope_tables_match_oracle():
     for grid in (2, 8, 32):
         c, s = E.eva02_rope_tables(grid, 16)

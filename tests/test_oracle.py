@@ -49,6 +49,20 @@ def brute_quant_row(w: np.ndarray) -> tuple[np.ndarray, np.float32]:
     return np.array(codes, np.int8), scale
 
 
+@pytest.mark.parametrize("block,k", [(1024, 1024), (128, 640), (128, 2816)])
+def test_rotate_rows64_is_the_block_hadamard_product(rng, block, k):
+    """The weight rotation's FWHT equals W @ blockdiag(H_block) formed by a float64 product, to float64 rounding; a
+    planted sign error in one butterfly stage is far outside that bound."""
+    w = (rng.standard_normal((48, k)) * 0.02).astype(F32)
+    got = OM.rotate_rows64(w, block)
+    want = w.astype(np.float64) @ OM.block_hadamard(k, block)
+    assert np.abs(got - want).max() <= 1e-13 * np.abs(want).max()
+    v = w.astype(np.float64).reshape(48, k // block, block // 2, 2)
+    bad = np.stack((v[..., 0] + v[..., 1], v[..., 1] - v[..., 0]), -1).reshape(48, k // block, block)  # wrong sign
+    bad = OM.rotate_rows64(bad.reshape(48, k), block)  # (stage 0 done twice: not the transform either)
+    assert np.abs(bad - want).max() > 1e-3 * np.abs(want).max()
+
+
 def test_quantize_rows_int8_brute_force(rng):
     w = rng.standard_normal((7, 33)).astype(F32) * 0.02
     w[1] = 0.0
@@ -340,8 +354,29 @@ def test_rope_tables_closed_form():
     assert cos.shape == (1025, 32) and (cos[0] == 1).all() and (sin[0] == 0).all()
     band = 1.0 / 10000 ** (np.arange(16) / 16)
     r, c = 5, 7  # token 1 + 5 * 32 + 7
-    np.testing.assert_allclose(cos[1 + r * 32 + c, :16], np.cos(r / 32 * 16 * band), atol=1e-7)
-    np.testing.assert_allclose(sin[1 + r * 32 + c, 16:], np.sin(c / 32 * 16 * band), atol=1e-7)
+    np.testing.assert_allclose(cos[1 + r * 32 + c, :16], np.cos(r / 32 * 16 * band), atol=2e-6)
+    np.testing.assert_allclose(sin[1 + r * 32 + c, 16:], np.sin(c / 32 * 16 * band), atol=2e-6)
+    # every entry against float64 angles: the float32 recipe stays within a few float32 roundings of the angle
+    # (|angle| <= 16), never a wrong band or position (a planted swap of rows and columns is off by O(1))
+    t = np.arange(32) / 32 * 16
+    ang = np.concatenate([np.repeat(t, 32)[:, None] * band, np.tile(t, 32)[:, None] * band], axis=1)
+    assert np.abs(cos[1:] - np.cos(ang)).max() < 4e-6 and np.abs(sin[1:] - np.sin(ang)).max() < 4e-6
+    swapped = np.concatenate([ang[:, 16:], ang[:, :16]], axis=1)
+    assert np.abs(cos[1:] - np.cos(swapped)).max() > 0.5
+
+
+def test_rope_tables_follow_the_float32_recipe():
+    """The tables are the reference's float32 computation (mlx/haruka.py:26-32) step for step, not a float64 one
+    rounded once: the two differ in the last bits of thousands of entries at grid 32 / ref 16."""
+    cos, sin = OM.eva02_rope_tables(32, 16)
+    band = 1.0 / 10000 ** (np.arange(16) / 16)
+    t = np.arange(32) / 32 * 16
+    ang = np.concatenate([np.repeat(t, 32)[:, None] * band, np.tile(t, 32)[:, None] * band], axis=1)
+    assert (cos[1:] != np.cos(ang).astype(F32)).sum() > 1000
+    b32 = F32(1.0) / (F32(10000.0) ** (np.arange(16, dtype=F32) / F32(16)))
+    t32 = np.arange(32, dtype=F32) / F32(32) * F32(16)
+    a32 = (t32[5] * b32).astype(F32)
+    np.testing.assert_array_equal(cos[1 + 5 * 32 + 7, :16], np.cos(a32))
 
 
 def test_interleave_swiglu_layout(rng):

@@ -158,3 +158,49 @@ def test_oracle_int8_forward_within_float_budget():
     assert np.isfinite(p8).all() and p8.shape == (2, cfg.tags)
     err = np.abs(p8 - pf)
     assert err.max() < 0.05 and err.mean() < 0.01, (err.max(), err.mean())
+
+
+@pytest.mark.parametrize(("h", "w", "nh", "nw"), [(900, 1200, 84, 112), (37, 100, 41, 112), (20, 30, 75, 112),
+                                                (1200, 1200, 112, 112), (5, 3000, 1, 112), (1008, 700, 1008, 700)])
+def test_bilinear_aa_matrix_is_torch_antialiased_bilinear(h, w, nh, nw):
+    """The oracle's filter rows against torch's own interpolate(bilinear, antialias=True) on the CPU in float64 (the
+    function PixAI's preprocessing calls through torchvision, foidfinder/backends/cuda/preprocess.py:27-28):
+    downscales by 1 to 27, enlargements, a one-row output and the identity."""
+    import torch.nn.functional as F
+
+    from oracle import resample as ORS
+
+    x = np.random.default_rng(h * w).random((h, w, 3))
+    got = F.interpolate(torch.from_numpy(x).permute(2, 0, 1)[None], size=(nh, nw), mode="bilinear",
+                        align_corners=False, antialias=True)[0].permute(1, 2, 0).numpy()
+    want = ORS.resize_2d(x, ORS.bilinear_aa_matrix(h, nh), ORS.bilinear_aa_matrix(w, nw))
+    assert np.abs(got - want).max() < 1e-12
+    assert np.allclose(ORS.bilinear_aa_matrix(h, nh).sum(1), 1.0)
+
+
+def test_write_int8_dir_format(tmp_path):
+    """The converted PixAI directory (the reference's `foidfinder convert` output, cli.py:143-161): format metadata,
+    the reference's key set (engine.py:49-62) and the oracle's codes; a second conversion is refused."""
+    import json
+
+    from safetensors import safe_open
+    from safetensors.torch import save_file
+
+    from foidfinder_amd.pixai import synthetic_checkpoint, write_int8_dir
+
+    cfg, ocfg = small_cfgs()
+    raw = synthetic_checkpoint(cfg, seed=31)
+    src, out = tmp_path / "official", tmp_path / "int8"
+    src.mkdir()
+    save_file(raw, str(src / "model.safetensors"))
+    (src / "config.json").write_text(json.dumps(
+        {"num_classes": cfg.tags, "foidfinder_rocm": {"img_size": 112, "win": 4, "global_blocks": [1]}}))
+    write_int8_dir(src, out, device="cpu")
+    want = OP.convert_checkpoint({k: v.numpy() for k, v in raw.items()}, ocfg)
+    with safe_open(str(out / "model.safetensors"), "np") as f:
+        assert f.metadata() == {"format": "foidfinder-pixai-int8-v1"}
+        assert set(f.keys()) == set(want)
+        for k in want:
+            assert np.array_equal(f.get_tensor(k), want[k]), k
+    with pytest.raises(RuntimeError, match="already in the int8 format"):
+        write_int8_dir(out, tmp_path / "again", device="cpu")

@@ -168,3 +168,48 @@ def test_rocm_backend_serves_a_pixai_model_dir(dev, tmp_path):
                                                    "tags": ["a"]}))
     with pytest.raises(RuntimeError, match="unsupported model architecture"):
         backends.load("rocm", other)
+
+
+PREPROCESS_CASES = [(900, 1200), (1200, 900), (448, 900), (300, 1500), (37, 100), (60, 45), (112, 112), (3, 400)]
+
+
+@pytest.mark.parametrize(("h", "w"), PREPROCESS_CASES)
+def test_preprocess_matches_the_letterbox_restatement(dev, h, w):
+    """backends/rocm/preprocess.py:preprocess (PixAI's letterbox on the GPU) against the float64 restatement of the
+    reference's recipe (foidfinder/backends/cuda/preprocess.py:16-32: white compositing, antialiased bilinear resize
+    of the longer side to the input size, [-1, 1] normalization, -1 padding): downscales, wide and tall images, an
+    enlargement, the identity size and a 3-pixel-high strip. The bar: every pixel within half an fp16 ulp of the
+    float64 value plus 2e-5 (the GPU's float32 weights and sums), the padding exactly -1."""
+    from PIL import Image
+
+    from foidfinder_amd.backends.rocm.preprocess import preprocess
+    from oracle import resample as ORS
+
+    size = 112
+    rgb = np.random.default_rng(h * 7 + w).integers(0, 256, (h, w, 3), dtype=np.uint8)
+    got = preprocess([Image.fromarray(rgb)], size, device=dev)[0].float().cpu().numpy().astype(np.float64)
+    want = ORS.letterbox_pixai(rgb, size)
+    bound = 0.5 * np.spacing(np.abs(want).astype(np.float16)).astype(np.float64) + 2e-5
+    assert (np.abs(got - want) <= bound).all(), np.abs(got - want).max()
+    assert np.array_equal(got[want == -1.0], want[want == -1.0])
+
+
+def test_preprocess_constant_and_transparent_images(dev):
+    """A constant image stays that constant (the filter rows sum to one); a transparent one becomes white (+1); a
+    grey image with half-transparent pixels is composited onto white first, as the reference's rgb_on_white."""
+    from PIL import Image
+
+    from foidfinder_amd.backends.rocm.preprocess import preprocess
+
+    grey = Image.fromarray(np.full((90, 140, 3), 100, np.uint8))
+    clear = Image.fromarray(np.zeros((50, 50, 4), np.uint8), "RGBA")
+    half = np.zeros((40, 40, 4), np.uint8)
+    half[..., :3], half[..., 3] = 0, 128
+    out = preprocess([grey, clear, Image.fromarray(half, "RGBA")], 112, device=dev).float().cpu().numpy()
+    nh = int(90 * 112 / 140)
+    top = (112 - nh) // 2
+    v = np.float16(100 / 255 * 2 - 1)
+    assert np.abs(out[0, top : top + nh] - v).max() <= 1e-3 and (out[0, :top] == -1).all()
+    assert (out[1] == 1.0).all()
+    comp = np.asarray(Image.alpha_composite(Image.new("RGBA", (40, 40), (255,) * 4), Image.fromarray(half, "RGBA")))
+    assert np.abs(out[2] - np.float16(comp[0, 0, 0] / 255 * 2 - 1)).max() <= 1e-3
