@@ -15,16 +15,17 @@
 // Per wave, S^T = K Q^T comes from v_mfma_f32_32x32x16_f16 with each lane holding one query and 16 of every 32 keys
 // (the other 16 sit in lane ^ 32), and P^T feeds the PV MFMA (O^T = V^T P^T) directly as its column operand. The
 // tile is processed in two 32-key halves (S, softmax, PV per half). At head_dim 64 the softmax, not the MFMA, bounds
-// the loop, so its common path is one exp2, half a convert and half a dot per score:
-//  * every S^T accumulator starts at -m_ref (the query's reference maximum, kept fp16-representable) through one
-//    extra MFMA whose operands hold 1 and -m_ref in a single k-slot; the first tile sets m_ref to its maximum;
-//  * p = v_exp_f32 (exp2), converted in pairs to fp16; each lane sums its fp16 p with fp32 dot2 (the same p that
-//    enter the PV product). While every lane's sum over a half stays <= SUM_LIMIT, every p <= SUM_LIMIT, which
-//    fp16 holds at full relative precision and fp32 accumulates far from overflow, so m_ref stays. Otherwise (rare:
-//    the scores rose well above m_ref) m_ref is raised to that half's maximum, O and l are rescaled by
-//    2^(m_old - m_new) and the half's p are recomputed.
+// the loop, so its common path is one exp2, half a convert and one add per score:
+//  * every S^T accumulator starts at -m_ref (the query's reference maximum, kept fp16-representable): a register
+//    block holding -m_ref is the C operand of each half's first product; the first tile sets m_ref to its maximum;
+//  * p = v_exp_f32 (exp2), converted in pairs to fp16 for the PV product; each lane sums its fp32 p with plain fp32
+//    adds (v_dot2 on the fp16 pairs shares the matrix core's issue and stalls behind its products; the fp32 sum differs
+//    from the sum of the fp16 p only by their unbiased roundings). While every lane's sum over a half stays
+//    <= SUM_LIMIT, every p <= SUM_LIMIT, which fp16 holds at full relative precision and fp32 accumulates far from
+//    overflow, so m_ref stays. Otherwise (rare: the scores rose well above m_ref) m_ref is raised to that half's
+//    maximum, O and l are rescaled by 2^(m_old - m_new) and the half's p are recomputed.
 // Tails: query rows >= L are computed on clamped rows and not stored; keys >= L (zero K rows) get S ~ -2^17 from
-// the same extra MFMA (see one_last below), so their p is exactly 0 with no masking instructions in the loop; when
+// an extra MFMA in the last tile (see last_operands below), so their p is exactly 0 with no masking instructions; when
 // the last tile's second half holds no key below L it is skipped. The last query block of a sequence, when it holds
 // at most two 32-query units (L = 1025 leaves one query), gives each unit two waves, one per key half, and merges
 // the two partial results through LDS at the end: that block then takes about half a block's time instead of a
@@ -150,61 +151,75 @@ __device__ __forceinline__ void attention_block(const half_t* __restrict__ qkv, 
   for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
-  // m_ref enters S through one extra MFMA per accumulator: the row operand `one_k` has 1 in k-slot 0 for every key,
-  // the column operand mq holds -m_ref (fp16) of the lane's query in k-slot 0, so the product starts every S^T
-  // accumulator at -m_ref. m_ref is kept fp16-representable (|m_ref| <= 65000). The last tile uses one_last[kh]
-  // instead, which also has 2 in k-slot 1 for keys >= L, against -65504 in k-slot 1 of mq: those keys start at
-  // -m_ref - 131008 < -66000, so exp2 gives exactly 0 (their K rows are zero). No branch or per-score select in the
-  // loop (the compiler turns a masked-tile branch into selects on every tile).
-  half8_t one_k = {}, one_last[2] = {{}, {}}, mq = {};
-  if (fh == 0) {
-    one_k[0] = static_cast<half_t>(1.f);
-#pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
-      one_last[kh][0] = static_cast<half_t>(1.f);
-      // key of this lane's row in the last tile: half kh (SPLIT: slot 0 is the wave's own half kh_sel)
-      const int key = (ntiles - 1) * BKV + (SPLIT ? kh_sel : kh) * 32 + fr;
-      one_last[kh][1] = static_cast<half_t>(key >= L ? 2.f : 0.f);
-    }
-    mq[1] = static_cast<half_t>(-65504.f);
-  }
   float m_ref = 0.f, l_run = 0.f;
-  const half2_t ones = {static_cast<half_t>(1.f), static_cast<half_t>(1.f)};
+  half_t m_ref_h = static_cast<half_t>(0.f);
+  float16_t negm = {};  // -m_ref in every accumulator slot (the lane's query)
   auto set_mref = [&](float m) __attribute__((always_inline)) {
     // smallest fp16 >= m (|m| < 65504): then every p of the tile that set it is <= 1
     const float mc = fminf(fmaxf(m, -65000.f), 65000.f);
-    half_t mh = static_cast<half_t>(mc + fabsf(mc) * 0.0009765625f + 6.103515625e-05f);
-    m_ref = static_cast<float>(mh);
-    if (fh == 0) mq[0] = -mh;
+    m_ref_h = static_cast<half_t>(mc + fabsf(mc) * 0.0009765625f + 6.103515625e-05f);
+    m_ref = static_cast<float>(m_ref_h);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) negm[r] = -m_ref;
+  };
+  // m_ref enters S as the C operand of each half's first product: negm holds -m_ref in every accumulator slot (the
+  // lane's query), kept fp16-representable (|m_ref| <= 65000). The last tile instead starts each half with one extra
+  // MFMA whose row operand has 1 in k-slot 0 for every key and 2 in k-slot 1 for keys >= L, against -m_ref and
+  // -65504 in the column operand's k-slots 0 and 1: keys past the sequence start at -m_ref - 131008 < -66000, so
+  // exp2 gives exactly 0 (their K rows are zero), with no per-score select. Those operands are built in the last
+  // tile only (no registers held through the loop).
+  auto last_operands = [&](int kh, half8_t& ok, half8_t& mq) __attribute__((always_inline)) {
+    ok = {};
+    mq = {};
+    if (fh == 0) {
+      ok[0] = static_cast<half_t>(1.f);
+      // key of this lane's row in the last tile: half kh (SPLIT: slot 0 is the wave's own half kh_sel)
+      const int key = (ntiles - 1) * BKV + (SPLIT ? kh_sel : kh) * 32 + fr;
+      ok[1] = static_cast<half_t>(key >= L ? 2.f : 0.f);
+      mq[0] = static_cast<half_t>(-m_ref_h);
+      mq[1] = static_cast<half_t>(-65504.f);
+    }
   };
 
-  float16_t xs[2];   // [kh]: S^T - m_ref, lane holds keys 32kh + 8(r/4) + 4fh + r%4
-  half8_t pf[2][2];  // [kh][tt]: fp16 p, slot u of lane half fh = key 32kh + 16tt + 8(u/4) + 4fh + u%4
-  float hs[2];       // [kh]: the lane's sum of its p over half kh
+  // One half's S and p at a time (the halves run one after the other, so one register block each suffices)
+  float16_t xs;    // S^T - m_ref of the current half kh: lane holds keys 32kh + 8(r/4) + 4fh + r%4
+  half8_t pf[2];   // [tt]: fp16 p, slot u of lane half fh = key 32kh + 16tt + 8(u/4) + 4fh + u%4
+  float hs[2];     // [kh]: the lane's sum of its p over half kh
   int ka[4], va[2];  // this tile's K and V read bases
 
   // Half kh of the tile (SPLIT: slot 0 is the wave's own half, whose rows koff/voff already select)
-  auto qk = [&](int kh, bool last) __attribute__((always_inline)) {
-    const float16_t zero = {};
-    const half8_t ok = last ? one_last[kh] : one_k;
-    xs[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ok, mq, zero, 0, 0, 0);
+  auto qk = [&](int kh, auto lastc) __attribute__((always_inline)) {
+    if constexpr (decltype(lastc)::value) {
+      const float16_t zero = {};
+      half8_t ok, mq;
+      last_operands(kh, ok, mq);
+      xs = __builtin_amdgcn_mfma_f32_32x32x16_f16(ok, mq, zero, 0, 0, 0);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const half8_t kf = *reinterpret_cast<const half8_t*>(smem + ka[s] + kh * 32 * HD);
-      xs[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], xs[kh], 0, 0, 0);
+      for (int s = 0; s < 4; ++s) {
+        const half8_t kf = *reinterpret_cast<const half8_t*>(smem + ka[s] + kh * 32 * HD);
+        xs = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], xs, 0, 0, 0);
+      }
+    } else {
+      // every other tile: -m_ref enters as the C operand of the first product (no extra MFMA)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const half8_t kf = *reinterpret_cast<const half8_t*>(smem + ka[s] + kh * 32 * HD);
+        xs = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], s == 0 ? negm : xs, 0, 0, 0);
+      }
     }
   };
   auto soft = [&](int kh) __attribute__((always_inline)) {
-    float acc = 0.f;
+    // two fp32 sum chains of the unrounded p (a v_dot2 on the fp16 pairs would queue behind the matrix core's work)
+    float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; r += 2) {
-      const half2_t p2 = {static_cast<half_t>(__builtin_amdgcn_exp2f(xs[kh][r])),
-                          static_cast<half_t>(__builtin_amdgcn_exp2f(xs[kh][r + 1]))};
-      acc = __builtin_amdgcn_fdot2(p2, ones, acc, false);
-      pf[kh][r >> 3][r & 7] = p2[0];
-      pf[kh][r >> 3][(r & 7) + 1] = p2[1];
+      const float e0 = __builtin_amdgcn_exp2f(xs[r]), e1 = __builtin_amdgcn_exp2f(xs[r + 1]);
+      acc0 += e0;
+      acc1 += e1;
+      pf[r >> 3][r & 7] = static_cast<half_t>(e0);
+      pf[r >> 3][(r & 7) + 1] = static_cast<half_t>(e1);
     }
-    hs[kh] = acc;
+    hs[kh] = acc0 + acc1;
   };
   auto pv = [&](auto khc) __attribute__((always_inline)) {
     constexpr int kh = decltype(khc)::value;
@@ -226,23 +241,23 @@ __device__ __forceinline__ void attention_block(const half_t* __restrict__ qkv, 
       for (int tt = 0; tt < 2; ++tt) {
         const half4_t lo = v[dt][tt][0], hi = v[dt][tt][1];
         const half8_t vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[kh][tt], o[dt], 0, 0, 0);
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[tt], o[dt], 0, 0, 0);
       }
   };
-  // Lane-pair maximum of xs[kh] (the query's 32 keys of half kh).
-  auto half_max = [&](int kh) __attribute__((always_inline)) {
-    float v = xs[kh][0];
+  // Lane-pair maximum of xs (the query's 32 keys of the current half).
+  auto half_max = [&]() __attribute__((always_inline)) {
+    float v = xs[0];
 #pragma unroll
-    for (int r = 1; r < 16; ++r) v = fmaxf(v, xs[kh][r]);
+    for (int r = 1; r < 16; ++r) v = fmaxf(v, xs[r]);
     return fmaxf(v, xor_shuffle(v, 32));
   };
   // Rare path of a half whose p overflowed the limit: raise m_ref to the maximum of S over that half (S recomputed
   // under the old m_ref), rescale O, l and the sum of half 0 when rescuing half 1, and recompute the half's S and p
   // under the new m_ref.
-  auto rescue = [&](int kh, bool last) __attribute__((always_inline)) {
-    qk(kh, last);
+  auto rescue = [&](int kh, auto lastc) __attribute__((always_inline)) {
+    qk(kh, lastc);
     const float m_old = m_ref;
-    const float mx = half_max(kh) + m_old;
+    const float mx = half_max() + m_old;
     if (mx > m_old) set_mref(mx);
     const float corr = __builtin_amdgcn_exp2f(m_old - m_ref);
     l_run *= corr;
@@ -251,14 +266,17 @@ __device__ __forceinline__ void attention_block(const half_t* __restrict__ qkv, 
     for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[dt][r] *= corr;
-    qk(kh, last);
+    qk(kh, lastc);
     soft(kh);
   };
 
 #pragma unroll
   for (int j = 0; j < STAGES - 1; ++j)
     if (j < ntiles) issue(j);
-  for (int tile = 0; tile < ntiles; ++tile) {
+  // One tile. LAST (the final tile, whose keys past L are masked by the extra MFMA) is a separate copy of the code,
+  // so the other tiles take -m_ref through the first product's C operand without a branch in their loop.
+  auto tile_body = [&](int tile, auto lastc) __attribute__((always_inline)) {
+    constexpr bool LAST = decltype(lastc)::value;
     // Tile `tile` has landed once at most the loads of the tiles issued after it are outstanding.
     if (tile + 1 < ntiles && STAGES > 2)
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LOADS * (STAGES - 2)) : "memory");
@@ -267,8 +285,7 @@ __device__ __forceinline__ void attention_block(const half_t* __restrict__ qkv, 
     __builtin_amdgcn_s_barrier();  // no fence: the vmcnt wait above already covers this thread's LDS writes
     // The ring slot of tile + STAGES - 1 was last read for tile - 1, which every wave has finished.
     if (tile + STAGES - 1 < ntiles) issue(tile + STAGES - 1);
-    const bool last = tile == ntiles - 1;
-    if (!active || (SPLIT && last && kh_sel == 1 && h1_empty)) continue;
+    if (!active || (SPLIT && LAST && kh_sel == 1 && h1_empty)) return;
     // Read bases, opaque to the compiler so that the fragment offsets fold into the reads' immediate offsets
     // instead of each being precomputed into a register.
     const int st = tile % STAGES;
@@ -282,31 +299,33 @@ __device__ __forceinline__ void attention_block(const half_t* __restrict__ qkv, 
       va[dt] = (STAGES + st) * TILE + voff[dt];
       asm volatile("" : "+v"(va[dt]));
     }
-    // One tile (a single copy of the code: per-variant copies of the MFMA regions make the register allocator
-    // shuffle the accumulators between them). Each half's p are checked (all lane sums <= SUM_LIMIT) before its PV
-    // product; the first tile sets m_ref from its maximum first.
-    qk(0, last);
+    // Each half's p are checked (all lane sums <= SUM_LIMIT) before its PV product; the first tile sets m_ref from
+    // its maximum first.
     if (tile == 0) {
+      qk(0, lastc);
       if constexpr (SPLIT) {
-        set_mref(half_max(0));
+        set_mref(half_max());
       } else {
-        qk(1, last);
-        set_mref(fmaxf(half_max(0), half_max(1)));
+        const float m0 = half_max();
+        qk(1, lastc);
+        set_mref(fmaxf(m0, half_max()));
       }
-      qk(0, last);
     }
+    qk(0, lastc);
     soft(0);
-    if (__any(hs[0] > SUM_LIMIT)) rescue(0, last);
+    if (__any(hs[0] > SUM_LIMIT)) rescue(0, lastc);
     pv(std::integral_constant<int, 0>{});
     hs[1] = 0.f;
-    if (!SPLIT && !(last && h1_empty)) {
-      qk(1, last);
+    if (!SPLIT && !(LAST && h1_empty)) {
+      qk(1, lastc);
       soft(1);
-      if (__any(hs[1] > SUM_LIMIT)) rescue(1, last);
+      if (__any(hs[1] > SUM_LIMIT)) rescue(1, lastc);
       pv(std::integral_constant<int, 1>{});
     }
     l_run += hs[0] + hs[1];
-  }
+  };
+  for (int tile = 0; tile + 1 < ntiles; ++tile) tile_body(tile, std::false_type{});
+  tile_body(ntiles - 1, std::true_type{});
 
   if constexpr (SPLIT) {
     // Merge: the half-1 wave of each unit leaves O, m_ref and l (per lane) in the LDS ring, free once every wave has
