@@ -7,7 +7,7 @@ EVA02-L/14-448 shapes (M = 32 800 tokens):
   * attention over 1025 tokens, 32 x 16 heads of 64: ff_attention and torch's scaled_dot_product_attention (fp16,
     whichever fused backend torch picks on this platform).
 
-    python -m foidfinder_amd.compare_libs [--batch 32] [--iters 20]
+    python -m foidfinder_amd.measure.compare_libs [--batch 32] [--iters 20]
 
 Times are per launch, from torch.cuda events around `iters` back-to-back launches on the current stream (every
 function here launches on it). Operands are random; nothing is checked (the tests do that).
@@ -20,8 +20,8 @@ import argparse
 import torch
 import torch.nn.functional as F
 
-from .engine import Eva02Config, eva02_rope_tables
-from .kernels import EPI_I32, EPI_QKV_ROPE, EPI_RESIDUAL, EPI_SWIGLU, kernels
+from ..engine import Eva02Config, eva02_rope_tables
+from ..kernels import EPI_I32, EPI_QKV_ROPE, EPI_RESIDUAL, EPI_SWIGLU, kernels
 
 INT8_PEAK, FP16_PEAK = 5.0e15, 2.5e15  # MI355X dense MFMA, ops/s
 

@@ -1,8 +1,8 @@
 """Launches each block kernel at the batch-32 EVA02-L/14-448 shapes, plus a plain copy of known size, for hardware
 counter runs (one counter set per run; `--only` narrows the launches to some of them):
 
-    rocprofv3 --pmc FETCH_SIZE -d <dir> -o fetch -- python -m foidfinder_amd.profile_kernels
-    rocprofv3 --pmc WRITE_SIZE -d <dir> -o write -- python -m foidfinder_amd.profile_kernels
+    rocprofv3 --pmc FETCH_SIZE -d <dir> -o fetch -- python -m foidfinder_amd.measure.profile_kernels
+    rocprofv3 --pmc WRITE_SIZE -d <dir> -o write -- python -m foidfinder_amd.measure.profile_kernels
 
 The copy (torch's elementwise copy of COPY_BYTES) calibrates the counters: HBM bytes of a kernel =
 counter_kib * 1024 * COPY_BYTES / copy_counter_bytes. Inputs are random, outputs scratch; nothing is checked here.
@@ -14,8 +14,8 @@ import argparse
 
 import torch
 
-from .engine import Eva02Config, eva02_rope_tables
-from .kernels import EPI_QKV_ROPE, EPI_RESIDUAL, EPI_SWIGLU, kernels, pad_norm
+from ..engine import Eva02Config, eva02_rope_tables
+from ..kernels import EPI_QKV_ROPE, EPI_RESIDUAL, EPI_SWIGLU, kernels, pad_norm
 
 COPY_BYTES = 1 << 30
 

@@ -90,9 +90,11 @@ def gelu_tanh(y: np.ndarray) -> np.ndarray:
 def exp_cw(x: np.ndarray) -> np.ndarray:
     """exp(x) in float32 from plain float32 operations in a fixed order: Cody-Waite range reduction x = n ln2 + r with
     ln2 split as 0.693145751953125 (16 significant bits, so n * head is exact for |n| < 256) + 1.428606765330187045e-6,
-    a degree-6 Taylor polynomial for e^r on |r| <= ln2/2 in Horner form, then an exact scaling by 2^n. This is the
-    SwiGLU epilogue's exp, chosen so the kernel and this restatement agree bit for bit (relative error below 3e-7
-    over [-80, 80], checked against float64 exp in tests/test_oracle.py)."""
+    a degree-6 Taylor polynomial for e^r on |r| <= ln2/2 in Horner form, then an exact scaling by 2^n: a
+    deterministic exp with relative error below 3e-7 over [-80, 80] (checked against float64 exp in
+    tests/test_oracle.py), so that the SwiGLU restatement does not depend on the host's libm. The kernel instead takes
+    e^-g from v_exp_f32 and the quotient from v_rcp_f32 (about 1 ulp each), so its fp16 SwiGLU outputs agree with
+    this restatement to within one fp16 ulp, not bit for bit; the SwiGLU parity tests allow exactly that."""
     x = np.asarray(x, F32)
     n = np.rint(x * F32(1.44269504088896341))
     r = (x - n * F32(0.693145751953125)) - n * F32(1.428606765330187045e-06)
