@@ -6,17 +6,19 @@
 // separately) - then the epilogue. The integer part is exact, so the order of the k-sum is free: each lane
 // feeds the MFMA 16 contiguous bytes of K and the A- and W-fragments use the same k slots.
 //
-// Both kernels use 256-thread workgroups (4 waves as 2 x 2), 64-byte K slices in LDS with the 16-byte chunks of
-// each 64-byte row XOR-swizzled by bits 2-3 of the row (conflict-free 16-byte fragment reads), and
-// v_mfma_i32_32x32x32_i8 computing the transposed product D[n][m] (the W fragment is the row operand), so each lane
-// ends with one output row m and runs of 4 consecutive columns n: the pair epilogues (RoPE, SwiGLU) stay inside a
-// lane and stores are 8 bytes wide.
+// Every variant computes the transposed product D[n][m] with v_mfma_i32_32x32x32_i8 (the W fragment is the row
+// operand), each wave a 128 x 64 (or 64 x 64) sub-tile, so each lane ends with one output row m and runs of 4
+// consecutive columns n: the pair epilogues (RoPE, SwiGLU) stay inside a lane, and the epilogue stages each wave's
+// rows through LDS for 16-byte stores. K slices sit in LDS with their 16-byte chunks XOR-swizzled by row bits
+// (conflict-free 16-byte fragment reads). The variant (the engine autotunes it per GEMM and batch size):
 //
-//  * gemm_s8_pipe_kernel (variant 1, large M): 256 x 256 tiles, each wave a 128 x 128 sub-tile (16 accumulator
-//    blocks in AGPRs), a 4-stage LDS ring filled by direct global->LDS loads (global_load_lds_dwordx4: no VGPR
-//    staging, 3 slices in flight). Tiles are ordered per XCD in groups of 4 m-tiles x 8 n-tiles so the 32 tiles an
-//    XCD runs at once share their A and W panels in its L2.
-//  * gemm_s8_kernel (variants 2, 3, small M): 128 x 128 or 256 x 128 tiles, register-staged double buffering.
+//  * 1, gemm_s8_kernel<128, 128>: 128 x 128 tiles, 4 waves, register-staged double buffering (small M).
+//  * 2, gemm_s8_ring_kernel: 256 x 128 tiles, 4 waves, a 3-slot ring of K-64 slices filled by buffer loads straight
+//    into LDS, two workgroups per CU.
+//  * 3, gemm_s8_wide_kernel: 256 x 256 tiles, 8 waves (2 per SIMD), one workgroup per CU, a 2-slot ring of K-128
+//    slices (4 slots of K 64 when K % 128 != 0).
+//  * 4, gemm_s8_persist_kernel: variant 3's main loop on a persistent grid of one workgroup per CU whose ring runs on
+//    across tiles, plus gemm_s8_tail_kernel for the rows past the last whole 256-row tile (large M).
 //
 // Reference: foidfinder/backends/cuda/csrc/gemm.cuh:14-171 and kernels.cu:167-217.
 #include <type_traits>
@@ -295,138 +297,9 @@ __device__ __forceinline__ void store_epilogue(const int16_t_v (&acc)[NI][MI], i
   }
 }
 
-// ---------------- variant 1: 256 x 256 tiles, 4-stage direct-to-LDS pipeline ----------------
-
-constexpr int P_BM = 256, P_BN = 256, P_STAGES = 4;
-constexpr int P_STAGE = (P_BM + P_BN) * BK;    // 32 KB per stage
-constexpr int P_LOADS = P_STAGE / (256 * 16);  // 16-byte loads per thread per stage (8)
-constexpr int P_GROUP_M = 4;                   // m-tiles per tile group (an XCD runs ~32 tiles at once)
-
 typedef __attribute__((address_space(3))) void lds_void;
 
-// Issues this thread's share of one K slice: rows of A (m0..m0+255) then W (n0..n0+255), 64 bytes each. A wave's
-// global_load_lds_dwordx4 writes 1 KB of LDS contiguously (lane l at +16 l), i.e. 16 rows; the lane reads the
-// global chunk that the swizzle places at its LDS position.
-__device__ __forceinline__ void pipe_issue(uint8_t* stage_base, const GemmArgs& a, int m0, int n0, int kt, int wave,
-                                           int lane) {
-  const int r16 = lane >> 2, pc = lane & 3;
-#pragma unroll
-  for (int p = 0; p < P_LOADS; ++p) {
-    const int blk = wave * P_LOADS + p;  // 1 KB block of the stage: 0..15 A rows, 16..31 W rows
-    const int row = (blk & 15) * 16 + r16;
-    const int lc = pc ^ ((row >> 2) & 3);  // the chunk swz() places at this lane's LDS position
-    const int8_t* src;
-    if (blk < 16) {
-      const int m = min(m0 + row, a.M - 1);
-      src = a.A + static_cast<int64_t>(m) * a.K + kt * BK + lc * 16;
-    } else {
-      const int n = min(n0 + row, a.N - 1);
-      src = a.W + static_cast<int64_t>(n) * a.K + kt * BK + lc * 16;
-    }
-    __builtin_amdgcn_global_load_lds(src, (lds_void*)(stage_base + blk * 1024), 16, 0, 0);
-  }
-}
-
-template <int EPI>
-__global__ __launch_bounds__(256, 1) void gemm_s8_pipe_kernel(const GemmArgs args) {
-  constexpr int WM = P_BM / 2, WN = P_BN / 2, MI = WM / 32, NI = WN / 32;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[P_STAGES * P_STAGE];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int tiles_m = (args.M + P_BM - 1) / P_BM, tiles_n = (args.N + P_BN - 1) / P_BN;
-  // logical tile -> (tm, tn): groups of P_GROUP_M m-tiles, m fastest within a group
-  const int t = xcd_remap(blockIdx.x, gridDim.x);
-  const int per_group = P_GROUP_M * tiles_n;
-  const int g = t / per_group, in_g = t % per_group;
-  const int gm = min(P_GROUP_M, tiles_m - g * P_GROUP_M);
-  const int tm = g * P_GROUP_M + in_g % gm, tn = in_g / gm;
-  const int m0 = tm * P_BM, n0 = tn * P_BN;
-  const int KT = args.K / BK;
-
-  int16_t_v acc[NI][MI];
-#pragma unroll
-  for (int i = 0; i < NI; ++i)
-#pragma unroll
-    for (int j = 0; j < MI; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-
-#pragma unroll
-  for (int s = 0; s < P_STAGES - 1; ++s)
-    if (s < KT) pipe_issue(smem + s * P_STAGE, args, m0, n0, s, wave, lane);
-
-  // Fragment reads are software-pipelined against the MFMAs: the second K half of slice kt is read while the first
-  // half's 16 MFMAs run, and the first half of slice kt+1 while the second half's run (2 MFMAs : 1 ds_read).
-  const int fr = lane & 31, fk = lane >> 5;
-  int4_t xw0[NI], ya0[MI], xw1[NI], ya1[MI];
-  auto read_half = [&](int slot, int kk, int4_t (&xw)[NI], int4_t (&ya)[MI]) {
-    const uint8_t* sa = smem + slot * P_STAGE;
-    const uint8_t* sw = sa + P_BM * BK;
-#pragma unroll
-    for (int i = 0; i < NI; ++i)
-      xw[i] = *reinterpret_cast<const int4_t*>(sw + swz(wn * WN + i * 32 + fr, 2 * kk + fk));
-#pragma unroll
-    for (int j = 0; j < MI; ++j)
-      ya[j] = *reinterpret_cast<const int4_t*>(sa + swz(wm * WM + j * 32 + fr, 2 * kk + fk));
-  };
-  auto mfma_half = [&](const int4_t (&xw)[NI], const int4_t (&ya)[MI]) {
-#pragma unroll
-    for (int i = 0; i < NI; ++i)
-#pragma unroll
-      for (int j = 0; j < MI; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xw[i], ya[j], acc[i][j], 0, 0, 0);
-  };
-  auto interleave = [] {
-#pragma unroll
-    for (int x = 0; x < NI + MI; ++x) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // 2 MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
-    }
-  };
-  auto barrier = [] {
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-  };
-
-  // Slice 0 is in LDS once this thread's loads of it are done and every thread has passed the barrier.
-  if (KT >= P_STAGES - 1)
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((P_STAGES - 2) * P_LOADS) : "memory");
-  else
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  barrier();
-  read_half(0, 0, xw0, ya0);
-
-  // One K slice. STEADY: slices kt+1..kt+P_STAGES-1 exist, so the refill of slot (kt-1) % P_STAGES (last read before
-  // the previous barrier) is issued and the wait for slice kt+1 may leave the newer (P_STAGES - 2) slices in flight;
-  // otherwise (the last P_STAGES - 1 slices) nothing is issued and the wait drains. Branch-free inside, so each half
-  // is one scheduling region. On the last slice the reads of "slice kt+1" hit a stale slot and are never used.
-  auto step = [&](int kt, auto steady) {
-    if constexpr (decltype(steady)::value)
-      pipe_issue(smem + ((kt + P_STAGES - 1) % P_STAGES) * P_STAGE, args, m0, n0, kt + P_STAGES - 1, wave, lane);
-    read_half(kt % P_STAGES, 1, xw1, ya1);
-    mfma_half(xw0, ya0);
-    interleave();
-    // This thread's reads of slot kt are complete before the barrier, so no thread refills it while it is read.
-    if constexpr (decltype(steady)::value)
-      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((P_STAGES - 2) * P_LOADS) : "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-    barrier();
-    read_half((kt + 1) % P_STAGES, 0, xw0, ya0);
-    mfma_half(xw1, ya1);
-    interleave();
-  };
-  int kt = 0;
-  for (; kt + P_STAGES - 1 < KT; ++kt) step(kt, std::true_type{});
-  for (; kt < KT; ++kt) step(kt, std::false_type{});
-  __syncthreads();  // every wave is done with the ring; reuse it as the epilogue staging area
-  static_assert(4 * stage_bytes<FF_EPI_QKV_ROPE, NI>() <= P_STAGES * P_STAGE, "staging must fit in the ring");
-  store_epilogue<EPI, NI, MI>(acc, m0 + wm * WM, n0 + wn * WN, lane, args,
-                              smem + wave * stage_bytes<EPI, NI>());
-}
-
-// ---------------- variant 4: 256 x 128 tiles, 3-stage buffer->LDS ring, 2 workgroups per CU ----------------
+// ---------------- variant 2: 256 x 128 tiles, 3-stage buffer->LDS ring, 2 workgroups per CU ----------------
 //
 // Sized for gfx950's feeds: an L2->CU load rate of ~55 B/clk per CU against 8192 int8 ops/clk per CU asks for
 // >= ~150 ops per loaded byte (a 256 x 128 tile gives 171), and each wave's 128 x 64 sub-tile needs 96 B/clk of the
@@ -620,7 +493,7 @@ static int launch_ring(const GemmArgs& a, int epi, hipStream_t st) {
   return check_launch("gemm_s8");
 }
 
-// ---------------- variants 6, 7: 256 x 256 tiles, 8 waves, buffer->LDS ring ----------------
+// ---------------- variant 3: 256 x 256 tiles, 8 waves, buffer->LDS ring ----------------
 //
 // Halves the load traffic per MFMA of the 256 x 128 ring (the CU's vector-memory path, not the MFMA, bounds that
 // kernel): 8 waves (2 per SIMD, each a 128 x 64 sub-tile as before) share one 256 x 256 tile, one workgroup per CU
@@ -780,9 +653,9 @@ static int launch_wide(const GemmArgs& a, int epi, hipStream_t st) {
   return check_launch("gemm_s8");
 }
 
-// ---------------- variant 8: persistent 256 x 256, 8 waves, one workgroup per CU ----------------
+// ---------------- variant 4: persistent 256 x 256, 8 waves, one workgroup per CU ----------------
 //
-// The variant-6 main loop (two 64 KB slots of K 128), with the ring running on across tiles: the grid holds one
+// The variant-3 main loop (two 64 KB slots of K 128), with the ring running on across tiles: the grid holds one
 // workgroup per CU, each takes every G-th tile of the grouped order, and slices are one stream, so the next tile's
 // first slice loads under the current tile's last MFMAs and its first fragments are read before the epilogue. No
 // workgroup starts cold, and row tiles that reach past M are ordered last (their rows past M load as zeros, and
@@ -940,7 +813,7 @@ __global__ __launch_bounds__(512, 1) void gemm_s8_persist_kernel(const GemmArgs 
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-// ---------------- the rows past the last whole 256-row tile (variant 8) ----------------
+// ---------------- the rows past the last whole 256-row tile (variant 4) ----------------
 //
 // M = 32 800 leaves 32 rows past 128 whole row tiles. As one more 256-row tile per column tile they would take a
 // whole extra round of the persistent grid (4 tiles on 4 CUs for N = 1024, each with the full K loop: ~24 us of
@@ -1065,7 +938,7 @@ static int launch_persist(const GemmArgs& args, int epi, hipStream_t st) {
   return launch_tail(args, whole, epi, st);
 }
 
-// ---------------- variants 2, 3: register-staged double buffering ----------------
+// ---------------- variant 1: 128 x 128 tiles, register-staged double buffering ----------------
 
 template <int BM, int BN, int EPI>
 __global__ __launch_bounds__(256) void gemm_s8_kernel(const GemmArgs args) {
@@ -1176,27 +1049,12 @@ static int launch_staged(const GemmArgs& a, int epi, hipStream_t st) {
   return check_launch("gemm_s8");
 }
 
-static int launch_pipe(const GemmArgs& a, int epi, hipStream_t st) {
-  const int64_t tiles = static_cast<int64_t>((a.M + P_BM - 1) / P_BM) * ((a.N + P_BN - 1) / P_BN);
-  if (tiles > 0x7fffffff) return fail(FF_EINVAL, "gemm_s8: too many tiles");
-  const dim3 grid(static_cast<unsigned>(tiles));
-  switch (epi) {
-    case FF_EPI_QKV_ROPE: gemm_s8_pipe_kernel<FF_EPI_QKV_ROPE><<<grid, 256, 0, st>>>(a); break;
-    case FF_EPI_RESIDUAL: gemm_s8_pipe_kernel<FF_EPI_RESIDUAL><<<grid, 256, 0, st>>>(a); break;
-    case FF_EPI_GELU_F16: gemm_s8_pipe_kernel<FF_EPI_GELU_F16><<<grid, 256, 0, st>>>(a); break;
-    case FF_EPI_SWIGLU: gemm_s8_pipe_kernel<FF_EPI_SWIGLU><<<grid, 256, 0, st>>>(a); break;
-    case FF_EPI_BIAS_F16: gemm_s8_pipe_kernel<FF_EPI_BIAS_F16><<<grid, 256, 0, st>>>(a); break;
-    case FF_EPI_I32: gemm_s8_pipe_kernel<FF_EPI_I32><<<grid, 256, 0, st>>>(a); break;
-    default: return fail(FF_EINVAL, "gemm_s8: bad epilogue");
-  }
-  return check_launch("gemm_s8");
-}
-
-// 1: 256 x 256 pipelined (direct-to-LDS, 4 stages); 2: 128 x 128 staged; 3: 256 x 128 staged;
-// 4, 5: 256 x 128 buffer->LDS ring, two workgroups per CU (3 slots of K 64, 6 slots of K 32);
-// 6, 7: 256 x 256, 8 waves, one workgroup per CU (2 slots of K 128 - or variant 7 when K % 128 != 0 -, 4 slots
-// of K 64); 8: variant 6 as a persistent grid, the ring streaming across tiles (variant 7 when K % 128 != 0).
-constexpr int kVariants = 8;
+// 1: 128 x 128 register-staged; 2: 256 x 128 buffer->LDS ring (3 slots of K 64), two workgroups per CU;
+// 3: 256 x 256, 8 waves, one workgroup per CU (2 slots of K 128, or 4 slots of K 64 when K % 128 != 0);
+// 4: variant 3 as a persistent grid, the ring streaming across tiles (4 slots of K 64, not persistent, when
+// K % 128 != 0). These are the variants the engine's autotune picks at the served shapes (1 for small M, 2 and 3 for
+// mid-sized M and the narrower GEMMs, 4 for large M).
+constexpr int kVariants = 4;
 
 }  // namespace ff
 
@@ -1248,16 +1106,12 @@ extern "C" int ff_gemm_s8(const int8_t* A, const int8_t* W, int64_t M, int64_t N
   a.rope_len = static_cast<int>(rope_len);
   a.q_scale = q_scale;
   hipStream_t st = as_stream(stream);
-  if (variant == 0) variant = M >= 4096 ? 1 : 2;
+  if (variant == 0) variant = M < 2048 ? 1 : (M < 16384 ? 2 : 4);
   switch (variant) {
-    case 1: return launch_pipe(a, epi, st);
-    case 2: return launch_staged<128, 128>(a, epi, st);
-    case 3: return launch_staged<256, 128>(a, epi, st);
-    case 4: return launch_ring<64, 3>(a, epi, st);
-    case 5: return launch_ring<32, 6>(a, epi, st);
-    case 6: return a.K % 128 == 0 ? launch_wide<128, 2>(a, epi, st) : launch_wide<64, 4>(a, epi, st);
-    case 7: return launch_wide<64, 4>(a, epi, st);
-    case 8: return a.K % 128 == 0 ? launch_persist(a, epi, st) : launch_wide<64, 4>(a, epi, st);
+    case 1: return launch_staged<128, 128>(a, epi, st);
+    case 2: return launch_ring<64, 3>(a, epi, st);
+    case 3: return a.K % 128 == 0 ? launch_wide<128, 2>(a, epi, st) : launch_wide<64, 4>(a, epi, st);
+    case 4: return a.K % 128 == 0 ? launch_persist(a, epi, st) : launch_wide<64, 4>(a, epi, st);
   }
   return fail(FF_EINVAL, "gemm_s8: bad variant");
 }
