@@ -18,7 +18,7 @@
 //  * 3, gemm_s8_wide_kernel: 256 x 256 tiles, 8 waves (2 per SIMD), one workgroup per CU, a 2-slot ring of K-128
 //    slices (4 slots of K 64 when K % 128 != 0).
 //  * 4, gemm_s8_persist_kernel: variant 3's main loop on a persistent grid of one workgroup per CU whose ring runs on
-//    across tiles, plus gemm_s8_tail_kernel for the rows past the last whole 256-row tile (large M).
+//    across tiles; the rows past the last whole 256-row tile follow in 32 x 32 blocks, split-K (large M).
 //
 // Reference: foidfinder/backends/cuda/csrc/gemm.cuh:14-171 and kernels.cu:167-217.
 #include <type_traits>
@@ -653,6 +653,84 @@ static int launch_wide(const GemmArgs& a, int epi, hipStream_t st) {
   return check_launch("gemm_s8");
 }
 
+// ---------------- the rows past the last whole 256-row tile (variant 4) ----------------
+//
+// M = 32 800 leaves 32 rows past 128 whole row tiles. As one more 256-row tile per column tile they would take a
+// whole extra round of the persistent grid (4 tiles on 4 CUs for N = 1024, each with the full K loop: ~24 us of
+// fc2's ~113 us). Instead, once its tiles are done, workgroup b of the persistent grid takes blocks b, b + G, ... of
+// 32 of those rows x 32 columns (a separate launch would cost a launch gap and a ramp per GEMM), and splits K over its
+// 8 waves in 128-byte chunks (wave w: chunks w, w + 8, ...). A wave stages each chunk of its 32 A rows and 32 W rows in its own two LDS
+// buffers with buffer->LDS loads (whole 128-byte rows per 8 lanes, the next chunk loading while the current one is
+// multiplied; rows past M or N read as zeros), the waves' int32 partial products are summed exactly through LDS, and
+// wave 0 applies the same epilogue as the main kernel. No barrier until the sum: each wave touches only its buffers.
+constexpr int T_CHUNK = 64 * 128;  // one staged chunk: 32 A rows + 32 W rows x 128 K bytes
+
+template <int EPI>
+__device__ __forceinline__ void tail_block(const GemmArgs& args, int m_first, int bx, int by, uint8_t* lds) {
+  // lds: 8 * 2 * T_CHUNK bytes, [wave][2 buffers][64 rows x 128 B]
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int fr = lane & 31, fk = lane >> 5;
+  const int M = args.M, N = args.N, K = args.K, nch = K / 128;
+  const int m0 = m_first + 32 * by, n0 = 32 * bx;
+  const int a_bytes = buf_bytes(static_cast<int64_t>(M - m0) * K), w_bytes = buf_bytes(static_cast<int64_t>(N - n0) * K);
+  const int8_t* abase = args.A + static_cast<int64_t>(m0) * K;
+  const int8_t* wbase = args.W + static_cast<int64_t>(n0) * K;
+  uint8_t* mine = lds + wave * 2 * T_CHUNK;
+  // Load p of a chunk fills LDS rows 8p .. 8p + 7 (rows 0-31: A, 32-63: W); lane l writes physical 16-byte slot l % 8
+  // of row 8p + l / 8, so it fetches the global chunk that the swizzle of wswz<128> puts there.
+  auto load_chunk = [&](int c, uint8_t* dst) __attribute__((always_inline)) {
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      const int row = 8 * p + (lane >> 3), slot = lane & 7;
+      const uint32_t voff =
+          static_cast<uint32_t>((row & 31) * K + c * 128 + ((slot ^ ((row >> 1) & 7)) << 4));
+      if (p < 4)
+        buffer_to_lds(abase, a_bytes, dst + p * 1024, voff);
+      else
+        buffer_to_lds(wbase, w_bytes, dst + p * 1024, voff);
+    }
+  };
+  int16_t_v acc[1][1] = {};
+  int b = 0;
+  if (wave < nch) load_chunk(wave, mine);
+  for (int c = wave; c < nch; c += 8, b ^= 1) {
+    if (c + 8 < nch) {
+      load_chunk(c + 8, mine + (b ^ 1) * T_CHUNK);  // that buffer's last reads finished in the previous chunk
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // chunk c has landed (only chunk c + 8's loads outstanding)
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    const uint8_t* sb = mine + b * T_CHUNK;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int4_t ya = *reinterpret_cast<const int4_t*>(sb + wswz<128>(fr, 2 * kk + fk));
+      const int4_t xw = *reinterpret_cast<const int4_t*>(sb + wswz<128>(32 + fr, 2 * kk + fk));
+      acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xw, ya, acc[0][0], 0, 0, 0);
+    }
+  }
+  // partial products: each wave into the start of its own buffers (its chunk reads are done)
+  int* part = reinterpret_cast<int*>(mine) + lane * 16;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    *reinterpret_cast<int4_t*>(part + 4 * q) =
+        int4_t{acc[0][0][4 * q], acc[0][0][4 * q + 1], acc[0][0][4 * q + 2], acc[0][0][4 * q + 3]};
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll 1
+  for (int w = 1; w < 8; ++w) {
+    const int* theirs = reinterpret_cast<const int*>(lds + w * 2 * T_CHUNK) + lane * 16;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int4_t v = *reinterpret_cast<const int4_t*>(theirs + 4 * q);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[0][0][4 * q + t] += v[t];
+    }
+  }
+  // every partial product is in wave 0's registers now: its own buffers are the epilogue's staging area
+  static_assert(stage_bytes<FF_EPI_QKV_ROPE, 1>() <= 2 * T_CHUNK, "staging must fit in wave 0's buffers");
+  store_epilogue<EPI, 1, 1>(acc, m0, n0, lane, args, lds);
+}
+
 // ---------------- variant 4: persistent 256 x 256, 8 waves, one workgroup per CU ----------------
 //
 // The variant-3 main loop (two 64 KB slots of K 128), with the ring running on across tiles: the grid holds one
@@ -664,7 +742,7 @@ static int launch_wide(const GemmArgs& a, int epi, hipStream_t st) {
 // staging areas do not fit in one slot (QKV), the last ones use a spare area past the ring.
 
 template <int EPI>
-__global__ __launch_bounds__(512, 1) void gemm_s8_persist_kernel(const GemmArgs args) {
+__global__ __launch_bounds__(512, 1) void gemm_s8_persist_kernel(const GemmArgs args, int m_full) {
   constexpr int RK = 128, BM = 256, BN = 256, WM = 128, WN = 64, MI = WM / 32, NI = WN / 32;
   constexpr int STAGE = (BM + BN) * RK;      // 64 KB per ring slot, two slots
   constexpr int LOADS = STAGE / (512 * 16);  // 16-byte loads per thread per slot
@@ -747,12 +825,13 @@ __global__ __launch_bounds__(512, 1) void gemm_s8_persist_kernel(const GemmArgs 
       ya[b][j] = *reinterpret_cast<const int4_t*>(sa + wswz<RK>(wm * WM + j * 32 + fr, 2 * kk + fk));
   };
 
-  if (total == 0) return;
-  issue();
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  read_frags(0, 0, 0);
-  int r = 0, m0, n0;
+  if (total > 0) {
+    issue();
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    read_frags(0, 0, 0);
+  }
+  int r = 0, m0 = 0, n0 = 0;
   coords(0, m0, n0);
   // Slice g: slice g + 1 is issued into the other slot (free: every wave passed the barrier after reading it);
   // the k-steps run in order, each while the next one's fragments are read; before the last one, slice g + 1 is
@@ -810,108 +889,27 @@ __global__ __launch_bounds__(512, 1) void gemm_s8_persist_kernel(const GemmArgs 
     read_frags(g, 0, 0);
     if (++r < my_tiles) coords(r, m0, n0);
   }
+  // The rows M .. m_full - 1 past the whole row tiles, in 32 x 32 blocks over the grid (see tail_block).
+  if (m_full > M) {
+    GemmArgs ta = args;
+    ta.M = m_full;
+    const int gx = (N + 31) / 32, nb = gx * ((m_full - M + 31) / 32);
+    for (int t = static_cast<int>(blockIdx.x); t < nb; t += G) {
+      __syncthreads();  // every wave is past its last reads of the LDS that tail_block now fills
+      tail_block<EPI>(ta, M, t % gx, t / gx, smem);
+    }
+  }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-}
-
-// ---------------- the rows past the last whole 256-row tile (variant 4) ----------------
-//
-// M = 32 800 leaves 32 rows past 128 whole row tiles. As one more 256-row tile per column tile they would take a
-// whole extra round of the persistent grid (4 tiles on 4 CUs for N = 1024, each with the full K loop: ~24 us of
-// fc2's ~113 us). Here each workgroup takes 32 of those rows x 32 columns and splits K over its 8 waves in 128-byte
-// chunks (wave w: chunks w, w + 8, ...). A wave stages each chunk of its 32 A rows and 32 W rows in its own two LDS
-// buffers with buffer->LDS loads (whole 128-byte rows per 8 lanes, the next chunk loading while the current one is
-// multiplied; rows past M or N read as zeros), the waves' int32 partial products are summed exactly through LDS, and
-// wave 0 applies the same epilogue as the main kernel. No barrier until the sum: each wave touches only its buffers.
-constexpr int T_CHUNK = 64 * 128;  // one staged chunk: 32 A rows + 32 W rows x 128 K bytes
-
-template <int EPI>
-__global__ __launch_bounds__(512) void gemm_s8_tail_kernel(const GemmArgs args, int m_first) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[8 * 2 * T_CHUNK];  // [wave][2 buffers][64 rows x 128 B]
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int fr = lane & 31, fk = lane >> 5;
-  const int M = args.M, N = args.N, K = args.K, nch = K / 128;
-  const int m0 = m_first + 32 * static_cast<int>(blockIdx.y), n0 = 32 * static_cast<int>(blockIdx.x);
-  const int a_bytes = buf_bytes(static_cast<int64_t>(M - m0) * K), w_bytes = buf_bytes(static_cast<int64_t>(N - n0) * K);
-  const int8_t* abase = args.A + static_cast<int64_t>(m0) * K;
-  const int8_t* wbase = args.W + static_cast<int64_t>(n0) * K;
-  uint8_t* mine = lds + wave * 2 * T_CHUNK;
-  // Load p of a chunk fills LDS rows 8p .. 8p + 7 (rows 0-31: A, 32-63: W); lane l writes physical 16-byte slot l % 8
-  // of row 8p + l / 8, so it fetches the global chunk that the swizzle of wswz<128> puts there.
-  auto load_chunk = [&](int c, uint8_t* dst) __attribute__((always_inline)) {
-#pragma unroll
-    for (int p = 0; p < 8; ++p) {
-      const int row = 8 * p + (lane >> 3), slot = lane & 7;
-      const uint32_t voff =
-          static_cast<uint32_t>((row & 31) * K + c * 128 + ((slot ^ ((row >> 1) & 7)) << 4));
-      if (p < 4)
-        buffer_to_lds(abase, a_bytes, dst + p * 1024, voff);
-      else
-        buffer_to_lds(wbase, w_bytes, dst + p * 1024, voff);
-    }
-  };
-  int16_t_v acc[1][1] = {};
-  int b = 0;
-  if (wave < nch) load_chunk(wave, mine);
-  for (int c = wave; c < nch; c += 8, b ^= 1) {
-    if (c + 8 < nch) {
-      load_chunk(c + 8, mine + (b ^ 1) * T_CHUNK);  // that buffer's last reads finished in the previous chunk
-      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // chunk c has landed (only chunk c + 8's loads outstanding)
-    } else {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-    const uint8_t* sb = mine + b * T_CHUNK;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int4_t ya = *reinterpret_cast<const int4_t*>(sb + wswz<128>(fr, 2 * kk + fk));
-      const int4_t xw = *reinterpret_cast<const int4_t*>(sb + wswz<128>(32 + fr, 2 * kk + fk));
-      acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xw, ya, acc[0][0], 0, 0, 0);
-    }
-  }
-  // partial products: each wave into the start of its own buffers (its chunk reads are done)
-  int* part = reinterpret_cast<int*>(mine) + lane * 16;
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-    *reinterpret_cast<int4_t*>(part + 4 * q) =
-        int4_t{acc[0][0][4 * q], acc[0][0][4 * q + 1], acc[0][0][4 * q + 2], acc[0][0][4 * q + 3]};
-  __syncthreads();
-  if (wave != 0) return;
-#pragma unroll 1
-  for (int w = 1; w < 8; ++w) {
-    const int* theirs = reinterpret_cast<const int*>(lds + w * 2 * T_CHUNK) + lane * 16;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int4_t v = *reinterpret_cast<const int4_t*>(theirs + 4 * q);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) acc[0][0][4 * q + t] += v[t];
-    }
-  }
-  // every partial product is in wave 0's registers now: its own buffers are the epilogue's staging area
-  static_assert(stage_bytes<FF_EPI_QKV_ROPE, 1>() <= 2 * T_CHUNK, "staging must fit in wave 0's buffers");
-  store_epilogue<EPI, 1, 1>(acc, m0, n0, lane, args, lds);
-}
-
-static int launch_tail(const GemmArgs& a, int m_first, int epi, hipStream_t st) {
-  const int rows = a.M - m_first;
-  const dim3 grid(static_cast<unsigned>((a.N + 31) / 32), static_cast<unsigned>((rows + 31) / 32));
-  switch (epi) {
-    case FF_EPI_QKV_ROPE: gemm_s8_tail_kernel<FF_EPI_QKV_ROPE><<<grid, 512, 0, st>>>(a, m_first); break;
-    case FF_EPI_RESIDUAL: gemm_s8_tail_kernel<FF_EPI_RESIDUAL><<<grid, 512, 0, st>>>(a, m_first); break;
-    case FF_EPI_GELU_F16: gemm_s8_tail_kernel<FF_EPI_GELU_F16><<<grid, 512, 0, st>>>(a, m_first); break;
-    case FF_EPI_SWIGLU: gemm_s8_tail_kernel<FF_EPI_SWIGLU><<<grid, 512, 0, st>>>(a, m_first); break;
-    case FF_EPI_BIAS_F16: gemm_s8_tail_kernel<FF_EPI_BIAS_F16><<<grid, 512, 0, st>>>(a, m_first); break;
-    case FF_EPI_I32: gemm_s8_tail_kernel<FF_EPI_I32><<<grid, 512, 0, st>>>(a, m_first); break;
-    default: return fail(FF_EINVAL, "gemm_s8: bad epilogue");
-  }
-  return check_launch("gemm_s8");
 }
 
 static int launch_persist(const GemmArgs& args, int epi, hipStream_t st) {
   if (args.K % 128 != 0) return fail(FF_EINVAL, "gemm_s8: K must be a multiple of the slice");
-  // Whole 256-row tiles on the persistent grid; the rows past them (if any) on the tail kernel, after it.
+  // Whole 256-row tiles on the persistent grid; the rows past them (if any) in 32-row blocks after its tiles.
   const int whole = args.M / 256 * 256;
   const bool split = whole > 0 && whole < args.M;
   GemmArgs a = args;
   if (split) a.M = whole;
+  const int m_full = args.M;
   const int64_t tiles = static_cast<int64_t>((a.M + 255) / 256) * ((a.N + 255) / 256);
   if (tiles > 0x7fffffff) return fail(FF_EINVAL, "gemm_s8: too many tiles");
   const void* kernels[] = {
@@ -926,16 +924,15 @@ static int launch_persist(const GemmArgs& args, int epi, hipStream_t st) {
   if (resident <= 0) resident = 256;
   const dim3 grid(static_cast<unsigned>(std::min<int64_t>(tiles, resident)));
   switch (epi) {
-    case FF_EPI_QKV_ROPE: gemm_s8_persist_kernel<FF_EPI_QKV_ROPE><<<grid, 512, 0, st>>>(a); break;
-    case FF_EPI_RESIDUAL: gemm_s8_persist_kernel<FF_EPI_RESIDUAL><<<grid, 512, 0, st>>>(a); break;
-    case FF_EPI_GELU_F16: gemm_s8_persist_kernel<FF_EPI_GELU_F16><<<grid, 512, 0, st>>>(a); break;
-    case FF_EPI_SWIGLU: gemm_s8_persist_kernel<FF_EPI_SWIGLU><<<grid, 512, 0, st>>>(a); break;
-    case FF_EPI_BIAS_F16: gemm_s8_persist_kernel<FF_EPI_BIAS_F16><<<grid, 512, 0, st>>>(a); break;
-    case FF_EPI_I32: gemm_s8_persist_kernel<FF_EPI_I32><<<grid, 512, 0, st>>>(a); break;
+    case FF_EPI_QKV_ROPE: gemm_s8_persist_kernel<FF_EPI_QKV_ROPE><<<grid, 512, 0, st>>>(a, m_full); break;
+    case FF_EPI_RESIDUAL: gemm_s8_persist_kernel<FF_EPI_RESIDUAL><<<grid, 512, 0, st>>>(a, m_full); break;
+    case FF_EPI_GELU_F16: gemm_s8_persist_kernel<FF_EPI_GELU_F16><<<grid, 512, 0, st>>>(a, m_full); break;
+    case FF_EPI_SWIGLU: gemm_s8_persist_kernel<FF_EPI_SWIGLU><<<grid, 512, 0, st>>>(a, m_full); break;
+    case FF_EPI_BIAS_F16: gemm_s8_persist_kernel<FF_EPI_BIAS_F16><<<grid, 512, 0, st>>>(a, m_full); break;
+    case FF_EPI_I32: gemm_s8_persist_kernel<FF_EPI_I32><<<grid, 512, 0, st>>>(a, m_full); break;
     default: return fail(FF_EINVAL, "gemm_s8: bad epilogue");
   }
-  if (const int rc = check_launch("gemm_s8"); rc != FF_OK || !split) return rc;
-  return launch_tail(args, whole, epi, st);
+  return check_launch("gemm_s8");
 }
 
 // ---------------- variant 1: 128 x 128 tiles, register-staged double buffering ----------------

@@ -24,7 +24,7 @@ def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--reps", type=int, default=3)
-    ap.add_argument("--variants", default="qkv=8,proj=8,fc1=8,fc2=8",
+    ap.add_argument("--variants", default="qkv=4,proj=4,fc1=4,fc2=4",
                     help="GEMM tile variant per GEMM, as the engine's autotune picked them (bench.py prints them)")
     ap.add_argument("--only", default="", help="comma-separated subset of: rot,gemm,attention,copy (default: all)")
     args = ap.parse_args()
