@@ -42,7 +42,7 @@ def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--iters", type=int, default=20)
-    ap.add_argument("--variant", type=int, default=8, help="ff_gemm_s8 tile variant (the engine's autotune pick)")
+    ap.add_argument("--variant", type=int, default=4, help="ff_gemm_s8 tile variant (the engine's autotune pick)")
     args = ap.parse_args()
     k = kernels()
     dev = torch.device("cuda:0")
