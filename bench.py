@@ -100,7 +100,7 @@ def kernel_table(eng, B: int, buf) -> dict:
         if bound == "hbm":
             ach, peak, unit = work / us / 1e3, PEAK_HBM_GBS, "GB/s"
         elif bound == "mfma_int8":
-            ach, peak, unit = work / us / 1e6, PEAK_INT8_TOPS, "TFLOP/s"
+            ach, peak, unit = work / us / 1e6, PEAK_INT8_TOPS, "TOP/s"
         else:
             ach, peak, unit = work / us / 1e6, PEAK_FP16_TFLOPS, "TFLOP/s"
         out[name] = {"us": round(us, 2), "launches_per_step": per_fwd, "work_per_launch": work,
@@ -261,7 +261,7 @@ def kernel_row(us: float, bound: str, work: int, per_fwd: int) -> dict:
     if bound == "hbm":
         ach, peak, unit = work / us / 1e3, PEAK_HBM_GBS, "GB/s"
     elif bound == "mfma_int8":
-        ach, peak, unit = work / us / 1e6, PEAK_INT8_TOPS, "TFLOP/s"
+        ach, peak, unit = work / us / 1e6, PEAK_INT8_TOPS, "TOP/s"
     else:
         ach, peak, unit = work / us / 1e6, PEAK_FP16_TFLOPS, "TFLOP/s"
     return {"us": round(us, 2), "launches_per_step": per_fwd, "work_per_launch": work, "achieved": round(ach, 1),
@@ -372,7 +372,8 @@ def bench_haruka(args) -> None:
                    f"{cfg.pool_heads} heads", "tags": cfg.tags, "parallelism": "single GPU"},
         "gemm_tops": round(gemm_tops, 1),
         "gemm_frac_of_int8_peak": round(gemm_tops / PEAK_INT8_TOPS, 4),
-        "roofline": {"kernel": dom, **{f: kern[dom][f] for f in ("bound", "achieved", "peak", "unit", "frac")}},
+        "roofline": {"kernel": dom, **{f: kern[dom][f] for f in ("bound", "achieved", "peak", "frac")},
+                     "unit": "GB/s" if kern[dom]["unit"] == "GB/s" else "TFLOP/s"},
         "kernels": kern,
         "gemm_variants": v,
         "work_per_step": {"gemm_int8_ops": sum(cfg.gemm_ops(B).values()), "attention_flops": cfg.attention_flops(B)},
@@ -464,7 +465,8 @@ def main():
         "gemm_tops": round(gemm_tops, 1),
         "gemm_frac_of_int8_peak": round(gemm_tops / PEAK_INT8_TOPS, 4),
         "roofline": {"kernel": dom, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
-                     "unit": dk["unit"], "frac": dk["frac"], "traffic": traffic},
+                     # the roofline object's unit is "GB/s" or "TFLOP/s"; int8 rates are tera-ops (2 per multiply-add)
+                     "unit": "GB/s" if dk["unit"] == "GB/s" else "TFLOP/s", "frac": dk["frac"], "traffic": traffic},
         "kernels": kern,
         "gemm_variants": {name: eng.variants.get((name, B), 0) for name in ("qkv", "proj", "fc1", "fc2")},
         "cpu_baseline": cpu,
