@@ -2,8 +2,8 @@
 
 Bars: int8 codes, fp32 row scales and int32 accumulators bit-exact; fp16 epilogues bias, residual and QKV+RoPE
 bit-exact; SwiGLU within one fp16 ulp (the GPU's silu uses its ~1-ulp exp and reciprocal units); GELU within 1e-3
-relative (the GPU's tanhf differs from numpy's by an ulp); attention within 4e-3 absolute of the float64 oracle (P is
-rounded to fp16 before the PV MFMA).
+relative (the GPU's tanhf differs from numpy's by an ulp); attention within 4e-3 absolute and 2e-3 relative per output
+row of the float64 oracle (P is rounded to fp16 before the PV MFMA).
 """
 
 from __future__ import annotations
@@ -255,6 +255,26 @@ def run_attention(dev, qkv, seq_len):
     return out.cpu().numpy()
 
 
+# Attention bars: 4e-3 absolute per element, and 2e-3 relative per output row (the L2 norm of one query's 64-value
+# output in one head), both against float64 attention on the same fp16 inputs. Expected error: the fp16 output
+# rounding (2^-11 = 4.9e-4 relative per element) and the fp16 P fed to the PV product while l sums the fp32 p (2^-11
+# relative per weight); measured up to 5.6e-4 row-relative (and 2.7e-3 absolute on the peaked-score cases).
+ATT_ABS, ATT_ROW_REL = 4e-3, 2e-3
+
+
+def check_attention(got, want, H):
+    """Asserts the attention bars; returns (max abs error, max row-relative error) for the report."""
+    assert np.isfinite(got).all()
+    err = np.abs(got - want)
+    d = (got - want).reshape(got.shape[0], H, 64)
+    ref = want.reshape(want.shape[0], H, 64)
+    rel = np.linalg.norm(d, axis=2) / np.maximum(np.linalg.norm(ref, axis=2), 1e-30)
+    print(f"attention: max abs err {err.max():.3e}, max row-relative err {rel.max():.3e}")
+    assert err.max() < ATT_ABS, f"max abs err {err.max()}"
+    assert rel.max() < ATT_ROW_REL, f"max row-relative err {rel.max()}"
+    return err.max(), rel.max()
+
+
 def qkv_inputs(rng, S, L, H):
     x = rng.standard_normal((S * L, 3 * H * 64), dtype=np.float32)
     x[:, : H * 64] *= np.float32(OM.Q_SCALE)
@@ -266,8 +286,7 @@ def test_attention_matches_float64(dev, rng, S, L, H):
     qkv = qkv_inputs(rng, S, L, H)
     got = run_attention(dev, qkv, L).astype(np.float64)
     want = OA.attention(qkv, L, out_dtype=np.float64)
-    err = np.abs(got - want).max()
-    assert np.isfinite(got).all() and err < 4e-3, f"max abs err {err}"
+    check_attention(got, want, H)
 
 
 # Short last query blocks (at most two 32-query units past the last full 128-query block), whose units are split
@@ -279,8 +298,7 @@ def test_attention_split_tail_blocks(dev, rng, S, L, H):
     qkv = qkv_inputs(rng, S, L, H)
     got = run_attention(dev, qkv, L).astype(np.float64)
     want = OA.attention(qkv, L, out_dtype=np.float64)
-    err = np.abs(got - want).max()
-    assert np.isfinite(got).all() and err < 4e-3, f"max abs err {err}"
+    check_attention(got, want, H)
 
 
 @pytest.mark.parametrize(("gain", "ramp"), [(8.0, 3.0), (30.0, 0.0), (4.0, 12.0)])
@@ -295,8 +313,7 @@ def test_attention_peaked_and_rising_scores(dev, rng, gain, ramp):
     qkv = qkv.astype(np.float16)
     got = run_attention(dev, qkv, L).astype(np.float64)
     want = OA.attention(qkv, L, out_dtype=np.float64)
-    err = np.abs(got - want).max()
-    assert np.isfinite(got).all() and err < 4e-3, f"max abs err {err}"
+    check_attention(got, want, H)
 
 
 def test_attention_identical_keys_give_mean_of_values(dev, rng):
