@@ -209,13 +209,14 @@ __device__ __forceinline__ void attention_block(const half_t* __restrict__ qkv, 
     }
   };
   auto soft = [&](int kh) __attribute__((always_inline)) {
-    // two fp32 sum chains of the unrounded p (a v_dot2 on the fp16 pairs would queue behind the matrix core's work)
+    // two fp32 sum chains of the unrounded p (a v_dot2 on the fp16 pairs would queue behind the matrix core's work),
+    // started from the first pair (0 + p is p for every p exp2 returns, but the compiler cannot drop that add)
     float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; r += 2) {
       const float e0 = __builtin_amdgcn_exp2f(xs[r]), e1 = __builtin_amdgcn_exp2f(xs[r + 1]);
-      acc0 += e0;
-      acc1 += e1;
+      acc0 = r == 0 ? e0 : acc0 + e0;
+      acc1 = r == 0 ? e1 : acc1 + e1;
       pf[r >> 3][r & 7] = static_cast<half_t>(e0);
       pf[r >> 3][(r & 7) + 1] = static_cast<half_t>(e1);
     }
