@@ -237,8 +237,11 @@ __global__ __launch_bounds__(256) void rot_q8_1024_kernel(const half_t* __restri
 // LayerNorm (new; EVA02's norm after SwiGLU): gamma/beta are [C] with zeros past c_real, held in LDS (dynamic, 2C
 // floats) for the workgroup's rows; sums over the real columns run per lane sequentially in (i, e) order, then over
 // the row's lanes by the xor tree 32 (G = 4 only), 16, 15, 7, 3, 1.
+// Rows of 9 or more lane groups of 8 columns (EVA02's 2816 at NI = 11) do not prefetch the next row: that frees 44
+// registers per lane, so three waves fit on a SIMD instead of two, and three waves issue the row's VALU work faster
+// than two waves can hide the load (measured 5-8 % faster at 32 800 x 2816); narrower rows keep the prefetch.
 template <int NI, bool NORM, int G>
-__global__ __launch_bounds__(256) void rot_q8_h128_kernel(const half_t* __restrict__ x, int64_t T, int C, int c_real,
+__global__ __launch_bounds__(256, NI > 8 ? 3 : 1) void rot_q8_h128_kernel(const half_t* __restrict__ x, int64_t T, int C, int c_real,
                                                           const float* __restrict__ gamma,
                                                           const float* __restrict__ beta, float eps,
                                                           int8_t* __restrict__ out, float* __restrict__ row_scale) {
@@ -257,6 +260,7 @@ __global__ __launch_bounds__(256) void rot_q8_h128_kernel(const half_t* __restri
   const int64_t stride = static_cast<int64_t>(gridDim.x) * 4 * RPW;
   // whole groups of 16 G lanes share a row; cross-lane operations below stay inside them
   int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * RPW + (G == 2 ? lane >> 5 : 0);
+  constexpr bool PF = NI <= 8;  // prefetch the next row
   half8_t nxt[NI];
   auto load = [&](int64_t r) __attribute__((always_inline)) {
 #pragma unroll
@@ -265,7 +269,7 @@ __global__ __launch_bounds__(256) void rot_q8_h128_kernel(const half_t* __restri
       nxt[i] = b < nb ? *reinterpret_cast<const half8_t*>(x + r * C + b * 128 + 8 * gl) : half8_t{};
     }
   };
-  if (row < T) load(row);
+  if (PF && row < T) load(row);
   int nreal[NI];  // real columns among the lane's 8 of block G i + g (a prefix)
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
@@ -285,11 +289,12 @@ __global__ __launch_bounds__(256) void rot_q8_h128_kernel(const half_t* __restri
   for (; row < T; row += stride) {
     float v[NI * 8];
     uint32_t w[NI][4];  // the row's fp16 pairs (column e in half e & 1 of word e / 2)
+    if (!PF) load(row);
 #pragma unroll
     for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int k = 0; k < 4; ++k) w[i][k] = __builtin_bit_cast(uint32_t, half2_t{nxt[i][2 * k], nxt[i][2 * k + 1]});
-    if (row + stride < T) load(row + stride);
+    if (PF && row + stride < T) load(row + stride);
     auto hv = [&](int i, int e, float s) __attribute__((always_inline)) {  // column (i, e) + s, one rounding
       return (e & 1) ? add_h<1>(w[i][e >> 1], s) : add_h<0>(w[i][e >> 1], s);
     };
