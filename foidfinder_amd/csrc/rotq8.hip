@@ -233,14 +233,13 @@ __global__ __launch_bounds__(256) void rot_q8_1024_kernel(const half_t* __restri
 // half-wave per row, two rows per wave), chosen so that no group idles (h128_groups). Lane 16g + l of a row owns,
 // for i = 0..NI-1, the 8 columns (G i + g)*128 + 8*gray(l) + e of block G i + g: column bits 0-2 in registers, bits
 // 3-6 across the 16 lanes of a DPP row. Stages run over column bits 0..6 in ascending order, as in
-// kernels.cu:125-135. 256-thread workgroups stride over the rows, each wave loading its next rows while it
-// transforms the current ones.
+// kernels.cu:125-135. 256-thread workgroups stride over the rows.
 // LayerNorm (new; EVA02's norm after SwiGLU): gamma/beta are [C] with zeros past c_real, held in LDS (dynamic, 2C
 // floats) for the workgroup's rows; sums over the real columns run per lane sequentially in (i, e) order, then over
 // the row's lanes by the xor tree 32 (G = 4 only), 16, 15, 7, 3, 1.
-// Rows of 9 or more lane groups of 8 columns (EVA02's 2816 at NI = 11) do not prefetch the next row: that frees 44
-// registers per lane, so three waves fit on a SIMD instead of two, and three waves issue the row's VALU work faster
-// than two waves can hide the load (measured 5-8 % faster at 32 800 x 2816); narrower rows keep the prefetch.
+// Rows are loaded at the top of their own iteration, not prefetched: the registers of a row in flight (8 NI per lane)
+// would cost occupancy, and more waves per SIMD hide the load better (at EVA02's 2816 columns, NI = 11, three waves
+// fit instead of two: 5-8 % faster; Haruka's rows 0-6 %).
 template <int NI, bool NORM, int G>
 __global__ __launch_bounds__(256, NI > 8 ? 3 : 1) void rot_q8_h128_kernel(const half_t* __restrict__ x, int64_t T, int C, int c_real,
                                                           const float* __restrict__ gamma,
@@ -261,7 +260,6 @@ __global__ __launch_bounds__(256, NI > 8 ? 3 : 1) void rot_q8_h128_kernel(const 
   const int64_t stride = static_cast<int64_t>(gridDim.x) * 4 * RPW;
   // whole groups of 16 G lanes share a row; cross-lane operations below stay inside them
   int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * RPW + (G == 2 ? lane >> 5 : 0);
-  constexpr bool PF = NI <= 8;  // prefetch the next row
   half8_t nxt[NI];
   auto load = [&](int64_t r) __attribute__((always_inline)) {
 #pragma unroll
@@ -270,7 +268,6 @@ __global__ __launch_bounds__(256, NI > 8 ? 3 : 1) void rot_q8_h128_kernel(const 
       nxt[i] = b < nb ? *reinterpret_cast<const half8_t*>(x + r * C + b * 128 + 8 * gl) : half8_t{};
     }
   };
-  if (PF && row < T) load(row);
   int nreal[NI];  // real columns among the lane's 8 of block G i + g (a prefix)
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
@@ -290,12 +287,11 @@ __global__ __launch_bounds__(256, NI > 8 ? 3 : 1) void rot_q8_h128_kernel(const 
   for (; row < T; row += stride) {
     float v[NI * 8];
     uint32_t w[NI][4];  // the row's fp16 pairs (column e in half e & 1 of word e / 2)
-    if (!PF) load(row);
+    load(row);
 #pragma unroll
     for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int k = 0; k < 4; ++k) w[i][k] = __builtin_bit_cast(uint32_t, half2_t{nxt[i][2 * k], nxt[i][2 * k + 1]});
-    if (PF && row + stride < T) load(row + stride);
     auto hv = [&](int i, int e, float s) __attribute__((always_inline)) {  // column (i, e) + s, one rounding
       return (e & 1) ? add_h<1>(w[i][e >> 1], s) : add_h<0>(w[i][e >> 1], s);
     };
