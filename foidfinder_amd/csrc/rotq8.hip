@@ -268,13 +268,9 @@ __global__ __launch_bounds__(256, NI > 8 ? 3 : 1) void rot_q8_h128_kernel(const 
       nxt[i] = b < nb ? *reinterpret_cast<const half8_t*>(x + r * C + b * 128 + 8 * gl) : half8_t{};
     }
   };
-  int nreal[NI];  // real columns among the lane's 8 of block G i + g (a prefix)
-#pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const int b = G * i + g;
-    const int left = c_real - (b * 128 + 8 * gl);
-    nreal[i] = b < nb ? (left < 0 ? 0 : (left > 8 ? 8 : left)) : 0;
-  }
+  // Real columns among the lane's 8 of block G i + g (a prefix): clamp(left0 - 128 G i, 0, 8). Blocks past the row
+  // end get 0 from the same formula (c_real <= 128 nb).
+  const int left0 = c_real - (g * 128 + 8 * gl);
   const float s3 = gray_sign(gl & 1), s4 = gray_sign(gl & 2), s5 = gray_sign(gl & 4), s6 = gray_sign(gl & 8);
   auto tree_sum = [](float t) __attribute__((always_inline)) {
     if constexpr (G == 4) t = t + xor_shuffle(t, 32);
@@ -297,14 +293,14 @@ __global__ __launch_bounds__(256, NI > 8 ? 3 : 1) void rot_q8_h128_kernel(const 
     };
     if constexpr (NORM) {
       // Only block groups past column c_real - 128 G can hold padding or the row end (uniform test): the others skip
-      // the masks. The per-lane counts are re-read opaquely each row so that the compiler cannot hoist 8 * NI
-      // loop-invariant lane masks into scalar registers (they would spill).
+      // the masks. The masked groups' counts come from one per-lane base re-read opaquely each row, so that the
+      // compiler neither hoists 8 NI loop-invariant lane masks into scalar registers nor holds NI counts in vector
+      // registers through the loop (at NI = 11 they spilled, and each reload waited for the row's loads).
+      int lb = left0;
+      asm volatile("" : "+v"(lb));
       int nr[NI];
 #pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        nr[i] = nreal[i];
-        asm volatile("" : "+v"(nr[i]));
-      }
+      for (int i = 0; i < NI; ++i) nr[i] = min(max(lb - 128 * G * i, 0), 8);
       float sum = 0.f;
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
