@@ -240,7 +240,7 @@ __global__ __launch_bounds__(256) void rot_q8_1024_kernel(const half_t* __restri
 // Rows are loaded at the top of their own iteration, not prefetched: the registers of a row in flight (8 NI per lane)
 // would cost occupancy, and more waves per SIMD hide the load better (at EVA02's 2816 columns, NI = 11, three waves
 // fit instead of two: 5-8 % faster; Haruka's rows 0-6 %).
-template <int NI, bool NORM, int G>
+template <int NI, bool NORM, int G, bool FULL>
 __global__ __launch_bounds__(256, NI > 8 ? 3 : 1) void rot_q8_h128_kernel(const half_t* __restrict__ x, int64_t T, int C, int c_real,
                                                           const float* __restrict__ gamma,
                                                           const float* __restrict__ beta, float eps,
@@ -265,7 +265,7 @@ __global__ __launch_bounds__(256, NI > 8 ? 3 : 1) void rot_q8_h128_kernel(const 
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int b = G * i + g;  // lanes of blocks past the row end hold zeros
-      nxt[i] = b < nb ? *reinterpret_cast<const half8_t*>(x + r * C + b * 128 + 8 * gl) : half8_t{};
+      nxt[i] = (FULL || b < nb) ? *reinterpret_cast<const half8_t*>(x + r * C + b * 128 + 8 * gl) : half8_t{};
     }
   };
   // Real columns among the lane's 8 of block G i + g (a prefix): clamp(left0 - 128 G i, 0, 8). Blocks past the row
@@ -417,19 +417,34 @@ static dim3 stride_grid(const void* kernel, size_t smem, int64_t T, int rows) {
 // 16-lane groups per row: 2 when the block count is even but not a multiple of 4 (768, 2816: no idle group), else 4
 static int h128_groups(int nb) { return nb % 2 == 0 && nb % 4 != 0 && nb / 2 <= 12 ? 2 : 4; }
 
-template <int NI, int G>
-static void launch_h128(hipStream_t st, const half_t* x, int64_t T, int C, int c_real, const float* g, const float* b,
-                        float eps, int8_t* out, float* rs) {
+template <int NI, int G, bool FULL>
+static void launch_h128_rows(hipStream_t st, const half_t* x, int64_t T, int C, int c_real, const float* g,
+                             const float* b, float eps, int8_t* out, float* rs) {
   const int rows_per_block = 4 * (4 / G);
   if (g) {
     const size_t smem = 2 * C * sizeof(float);
-    const dim3 grid = stride_grid(reinterpret_cast<const void*>(&rot_q8_h128_kernel<NI, true, G>), smem, T,
+    const dim3 grid = stride_grid(reinterpret_cast<const void*>(&rot_q8_h128_kernel<NI, true, G, FULL>), smem, T,
                                   rows_per_block);
-    rot_q8_h128_kernel<NI, true, G><<<grid, 256, smem, st>>>(x, T, C, c_real, g, b, eps, out, rs);
+    rot_q8_h128_kernel<NI, true, G, FULL><<<grid, 256, smem, st>>>(x, T, C, c_real, g, b, eps, out, rs);
   } else {
-    const dim3 grid = stride_grid(reinterpret_cast<const void*>(&rot_q8_h128_kernel<NI, false, G>), 0, T,
+    const dim3 grid = stride_grid(reinterpret_cast<const void*>(&rot_q8_h128_kernel<NI, false, G, FULL>), 0, T,
                                   rows_per_block);
-    rot_q8_h128_kernel<NI, false, G><<<grid, 256, 0, st>>>(x, T, C, c_real, g, b, eps, out, rs);
+    rot_q8_h128_kernel<NI, false, G, FULL><<<grid, 256, 0, st>>>(x, T, C, c_real, g, b, eps, out, rs);
+  }
+}
+// FULL: the row's nb blocks fill all NI G lane groups, so every load is unconditional (straight-line loads let the
+// compiler wait for each block group as it arrives instead of for the whole row before the first add). Half-wave
+// rows (G = 2) are always full; wave rows are full when 4 divides nb.
+template <int NI, int G>
+static void launch_h128(hipStream_t st, const half_t* x, int64_t T, int C, int c_real, const float* g, const float* b,
+                        float eps, int8_t* out, float* rs) {
+  if constexpr (G == 2) {
+    launch_h128_rows<NI, G, true>(st, x, T, C, c_real, g, b, eps, out, rs);
+  } else {
+    if ((C >> 7) == NI * G)
+      launch_h128_rows<NI, G, true>(st, x, T, C, c_real, g, b, eps, out, rs);
+    else
+      launch_h128_rows<NI, G, false>(st, x, T, C, c_real, g, b, eps, out, rs);
   }
 }
 
