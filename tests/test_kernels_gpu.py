@@ -100,14 +100,14 @@ def run_h128(x, dev, c_real=0, gamma=None, beta=None, eps=1e-6):
     return out.cpu().numpy(), rs.cpu().numpy()
 
 
-@pytest.mark.parametrize("C", [128, 640, 768, 2816, 4736])
+@pytest.mark.parametrize("C", [128, 512, 640, 768, 2048, 2816, 4736])
 @pytest.mark.parametrize("T", [1, 5, 300])
 def test_rot_q8_h128_bit_exact(dev, rng, T, C):
     x = activations(rng, T, C)
     assert_codes_equal(run_h128(x, dev), OR.rot_q8_h128(x), f"h128 T={T} C={C}")
 
 
-@pytest.mark.parametrize(("C", "c_real"), [(2816, 2730), (768, 768), (4736, 4736), (256, 130)])
+@pytest.mark.parametrize(("C", "c_real"), [(2816, 2730), (768, 768), (2048, 2048), (1024, 1000), (4736, 4736), (256, 130)])
 def test_rot_q8_h128_layernorm_bit_exact(dev, rng, C, c_real):
     x = activations(rng, 257, C)
     x[:, c_real:] = 0
