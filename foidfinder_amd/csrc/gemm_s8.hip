@@ -330,8 +330,8 @@ __device__ __forceinline__ void buffer_to_lds(const void* base, int nbytes, uint
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds_dst, 16, voff, 0, 0, 0);
 }
 
-// RK: K bytes per ring slot (64 or 32), S: ring depth. The prefetch distance is S - 2 slots (plus half a slot for
-// RK = 64), so RK = 32 with 6 slots doubles it in the same 72 KB.
+// RK: K bytes per ring slot, S: ring depth (variant 2 runs RK = 64, S = 3: 72 KB). The prefetch distance is S - 2
+// slots plus half a slot.
 template <int EPI, int RK, int S>
 __global__ __launch_bounds__(256, 2) void gemm_s8_ring_kernel(const GemmArgs args) {
   constexpr int WM = R_BM / 2, WN = R_BN / 2, MI = WM / 32, NI = WN / 32;

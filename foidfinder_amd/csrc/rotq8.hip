@@ -407,7 +407,7 @@ __global__ __launch_bounds__(256, NI > 8 ? 3 : 1) void rot_q8_h128_kernel(const 
 }
 
 // Grid of a grid-stride rotation kernel: one workgroup per `rows` rows, capped at what the device holds resident
-// (every workgroup then streams rows with its next row's loads in flight, and no workgroup waits for a slot).
+// (every workgroup then streams rows, and no workgroup waits for a slot).
 static dim3 stride_grid(const void* kernel, size_t smem, int64_t T, int rows) {
   int64_t cap = resident_blocks(kernel, 256, smem);
   if (cap <= 0) cap = 2048;
