@@ -27,9 +27,9 @@
 // Tails: query rows >= L are computed on clamped rows and not stored; keys >= L (zero K rows) get S ~ -2^17 from
 // an extra MFMA in the last tile (see last_operands below), so their p is exactly 0 with no masking instructions; when
 // the last tile's second half holds no key below L it is skipped. The last query block of a sequence, when it holds
-// at most two 32-query units (L = 1025 leaves one query), gives each unit two waves, one per key half, and merges
-// the two partial results through LDS at the end: that block then takes about half a block's time instead of a
-// whole block's with three of its four waves idle.
+// two 32-query units, gives each unit two waves, one per key half; when it holds one (L = 1025 leaves one query), all
+// four waves share it, each over one key half of every other tile. The partial results are merged through LDS at the
+// end, so that block takes about a quarter of a block's time instead of a whole block's with three waves idle.
 //
 // Reference: foidfinder/backends/cuda/csrc/attention.cuh:19-157 (which accumulates each 64-key block in fp16 and
 // rescales every block; here every product and sum is fp32).
@@ -52,8 +52,8 @@ constexpr int KPW = 8 / WAVES;        // 1 KB blocks of each K (and V) tile load
 constexpr int LOADS = 2 * KPW;        // buffer->LDS loads per thread per tile
 constexpr float SUM_LIMIT = 8192.f;   // per-lane half-tile sum of p above which m_ref is raised
 constexpr uint32_t RSRC_WORD3 = 0x00020000;  // buffer descriptor word 3: raw dword access (gfx9 family)
-constexpr int MERGE_WORDS = 34;       // floats per lane of a half-1 wave's partial result: O (32), m_ref, l
-static_assert(WAVES / 2 * MERGE_WORDS * 64 * 4 <= 2 * STAGES * TILE * 2, "merge area exceeds the LDS ring");
+constexpr int MERGE_WORDS = 34;       // floats per lane of a merged wave's partial result: O (32), m_ref, l
+static_assert((WAVES - 1) * MERGE_WORDS * 64 * 4 <= 2 * STAGES * TILE * 2, "merge area exceeds the LDS ring");
 
 // Physical 16-byte slot of chunk c in row r. K rows are read 16 rows per ds_read_b128 pass: XOR with bits 1-3 of the
 // row spreads them over all 64 banks. V rows are read by the transposing b64 read, 4 rows x 64 B per 32-lane pass:
@@ -70,10 +70,11 @@ __device__ __forceinline__ void tr_read(half4_t& v, uint32_t lds_addr) {
   asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(lds_addr), "n"(OFF) : "memory");
 }
 
-// One workgroup's work. SPLIT = false: wave w owns queries qb*BQ + 32w .. +31 over both key halves of every tile.
-// SPLIT = true (short last block): waves 2u and 2u + 1 share query unit u, each over one key half (kh_sel = w & 1);
-// the half-1 wave's O, m_ref and l are merged into its partner's at the end.
-template <bool SPLIT>
+// One workgroup's work. SPLIT = 0: wave w owns queries qb*BQ + 32w .. +31 over both key halves of every tile.
+// SPLIT = 1 (last block of two units): waves 2u and 2u + 1 share query unit u, each over one key half (kh_sel = w & 1);
+// the half-1 wave's O, m_ref and l are merged into its partner's at the end. SPLIT = 2 (last block of one unit): all
+// four waves share unit 0, wave w over key half w & 1 of the tiles of parity w >> 1; waves 1-3 are merged into wave 0.
+template <int SPLIT>
 __device__ __forceinline__ void attention_block(const half_t* __restrict__ qkv, half_t* __restrict__ out, int L,
                                                 int H, int qb, int h, int seq, half_t* smem) {
   const uint32_t smem_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)smem));
@@ -85,8 +86,10 @@ __device__ __forceinline__ void attention_block(const half_t* __restrict__ qkv, 
   const half_t* kbase = qbase + C;
   const half_t* vbase = qbase + 2 * C;
 
-  const int unit = SPLIT ? wave >> 1 : wave;
+  const int unit = SPLIT == 2 ? 0 : (SPLIT ? wave >> 1 : wave);
   const int kh_sel = SPLIT ? wave & 1 : 0;
+  const int first_tile = SPLIT == 2 ? wave >> 1 : 0;  // SPLIT 2: the wave computes tiles first_tile, +2, ...
+  bool seen = false;                                   // the wave has computed a tile (it has keys to merge)
   const int q0 = qb * BQ + unit * QW;
   const bool active = q0 < L;  // a wave whose queries all lie past L only helps load K and V
   const int ntiles = (L + BKV - 1) / BKV;
@@ -287,6 +290,7 @@ __device__ __forceinline__ void attention_block(const half_t* __restrict__ qkv, 
     // The ring slot of tile + STAGES - 1 was last read for tile - 1, which every wave has finished.
     if (tile + STAGES - 1 < ntiles) issue(tile + STAGES - 1);
     if (!active || (SPLIT && LAST && kh_sel == 1 && h1_empty)) return;
+    if (SPLIT == 2 && (tile & 1) != first_tile) return;
     // Read bases, opaque to the compiler so that the fragment offsets fold into the reads' immediate offsets
     // instead of each being precomputed into a register.
     const int st = tile % STAGES;
@@ -300,9 +304,9 @@ __device__ __forceinline__ void attention_block(const half_t* __restrict__ qkv, 
       va[dt] = (STAGES + st) * TILE + voff[dt];
       asm volatile("" : "+v"(va[dt]));
     }
-    // Each half's p are checked (all lane sums <= SUM_LIMIT) before its PV product; the first tile sets m_ref from
-    // its maximum first.
-    if (tile == 0) {
+    // Each half's p are checked (all lane sums <= SUM_LIMIT) before its PV product; the wave's first tile sets m_ref
+    // from its maximum first.
+    if (tile == first_tile) {
       qk(0, lastc);
       if constexpr (SPLIT) {
         set_mref(half_max());
@@ -324,33 +328,48 @@ __device__ __forceinline__ void attention_block(const half_t* __restrict__ qkv, 
       pv(std::integral_constant<int, 1>{});
     }
     l_run += hs[0] + hs[1];
+    seen = true;
   };
   for (int tile = 0; tile + 1 < ntiles; ++tile) tile_body(tile, std::false_type{});
   tile_body(ntiles - 1, std::true_type{});
 
   if constexpr (SPLIT) {
-    // Merge: the half-1 wave of each unit leaves O, m_ref and l (per lane) in the LDS ring, free once every wave has
-    // passed its last tile; a half-1 wave that saw no key (one tile, second half empty) leaves m = -inf.
-    float* comb = reinterpret_cast<float*>(smem) + unit * MERGE_WORDS * 64 + lane;
+    // Merge: every wave of a unit but its first (part 0) leaves O, m_ref and l (per lane) in the LDS ring, free once
+    // every wave has passed its last tile; a wave that computed no tile (its keys all lie past L) leaves m = -inf.
+    constexpr int SHARE = SPLIT == 2 ? WAVES : 2;  // waves per unit
+    const int part = SPLIT == 2 ? wave : kh_sel;
+    float* comb = reinterpret_cast<float*>(smem) + unit * (SHARE - 1) * MERGE_WORDS * 64 + lane;
     __syncthreads();
-    if (active && kh_sel == 1) {
+    if (active && part != 0) {
+      float* mine = comb + (part - 1) * MERGE_WORDS * 64;
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) comb[(dt * 16 + r) * 64] = o[dt][r];
-      comb[32 * 64] = h1_empty && ntiles == 1 ? -__builtin_inff() : m_ref;
-      comb[33 * 64] = l_run;
+        for (int r = 0; r < 16; ++r) mine[(dt * 16 + r) * 64] = o[dt][r];
+      mine[32 * 64] = seen ? m_ref : -__builtin_inff();
+      mine[33 * 64] = l_run;
     }
     __syncthreads();
-    if (!active || kh_sel == 1) return;
-    const float m1 = comb[32 * 64], l1 = comb[33 * 64];
-    const float m = fmaxf(m_ref, m1);
-    const float c0 = __builtin_amdgcn_exp2f(m_ref - m), c1 = __builtin_amdgcn_exp2f(m1 - m);
-    l_run = l_run * c0 + l1 * c1;
+    if (!active || part != 0) return;
+    float m = m_ref;
+#pragma unroll
+    for (int k = 1; k < SHARE; ++k) m = fmaxf(m, comb[((k - 1) * MERGE_WORDS + 32) * 64]);
+    const float c0 = __builtin_amdgcn_exp2f(m_ref - m);
+    l_run = l_run * c0;
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] * c0 + comb[(dt * 16 + r) * 64] * c1;
+      for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] * c0;
+#pragma unroll
+    for (int k = 1; k < SHARE; ++k) {
+      const float* theirs = comb + (k - 1) * MERGE_WORDS * 64;
+      const float ck = __builtin_amdgcn_exp2f(theirs[32 * 64] - m);
+      l_run = l_run + theirs[33 * 64] * ck;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] + theirs[(dt * 16 + r) * 64] * ck;
+    }
   } else {
     if (!active) return;
   }
@@ -382,10 +401,12 @@ __global__ __launch_bounds__(64 * WAVES, 4) void attention_kernel(const half_t* 
   const int t = xcd_remap(blockIdx.x, gridDim.x);
   const int qb = t % nq, h = (t / nq) % H, seq = t / (nq * H);
   const int units = min(WAVES, (L - qb * BQ + QW - 1) / QW);  // 32-query units of this block
-  if (2 * units <= WAVES)
-    attention_block<true>(qkv, out, L, H, qb, h, seq, smem);
+  if (units == 1)
+    attention_block<2>(qkv, out, L, H, qb, h, seq, smem);
+  else if (2 * units <= WAVES)
+    attention_block<1>(qkv, out, L, H, qb, h, seq, smem);
   else
-    attention_block<false>(qkv, out, L, H, qb, h, seq, smem);
+    attention_block<0>(qkv, out, L, H, qb, h, seq, smem);
 }
 
 }  // namespace ff
