@@ -289,11 +289,14 @@ def test_attention_matches_float64(dev, rng, S, L, H):
     check_attention(got, want, H)
 
 
-# Short last query blocks (at most two 32-query units past the last full 128-query block), whose units are split
-# over two waves by key half and merged: one or two units, the last tile's second key half empty (L mod 64 in
-# 1..32) or not, a single key tile, and PixAI's window (576) and grid (5184) lengths.
+# Short last query blocks (at most two 32-query units past the last full 128-query block): two units are split over
+# two waves each by key half, one unit over all four waves by key half and tile parity, and the partial results are
+# merged. Covered: one or two units, the last tile's second key half empty (L mod 64 in 1..32) or not, a single key
+# tile, waves that compute no tile at all (L 32, 2, 65: the odd tiles or the last second half hold no key), and
+# PixAI's window (576) and grid (5184) lengths.
 @pytest.mark.parametrize(("S", "L", "H"), [(2, 161, 4), (3, 33, 2), (2, 32, 2), (1, 168, 3), (4, 576, 2),
-                                           (1, 5184, 1), (2, 2, 2), (1, 190, 2)])
+                                           (1, 5184, 1), (2, 2, 2), (1, 190, 2), (2, 129, 2), (2, 65, 3), (1, 97, 2),
+                                           (1, 257, 2)])
 def test_attention_split_tail_blocks(dev, rng, S, L, H):
     qkv = qkv_inputs(rng, S, L, H)
     got = run_attention(dev, qkv, L).astype(np.float64)
