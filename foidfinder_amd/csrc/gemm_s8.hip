@@ -657,7 +657,7 @@ static int launch_wide(const GemmArgs& a, int epi, hipStream_t st) {
 //
 // M = 32 800 leaves 32 rows past 128 whole row tiles. As one more 256-row tile per column tile they would take a
 // whole extra round of the persistent grid (4 tiles on 4 CUs for N = 1024, each with the full K loop: ~24 us of
-// fc2's ~113 us). Instead, once its tiles are done, workgroup b of the persistent grid takes blocks b, b + G, ... of
+// fc2's ~113 us). Instead, before its tiles, workgroup b of the persistent grid takes blocks b, b + G, ... of
 // 32 of those rows x 32 columns (a separate launch would cost a launch gap and a ramp per GEMM), and splits K over its
 // 8 waves in 128-byte chunks (wave w: chunks w, w + 8, ...). A wave stages each chunk of its 32 A rows and 32 W rows in its own two LDS
 // buffers with buffer->LDS loads (whole 128-byte rows per 8 lanes, the next chunk loading while the current one is
@@ -825,6 +825,22 @@ __global__ __launch_bounds__(512, 1) void gemm_s8_persist_kernel(const GemmArgs 
       ya[b][j] = *reinterpret_cast<const int4_t*>(sa + wswz<RK>(wm * WM + j * 32 + fr, 2 * kk + fk));
   };
 
+  // The rows M .. m_full - 1 past the whole row tiles, in 32 x 32 blocks over the grid (see tail_block), before the
+  // tiles: after them, a block's first wait on its loads would also wait for the stores of the workgroup's last
+  // tile (a wave's memory operations complete in order), i.e. for the drain of every CU's last output burst.
+  if (m_full > M) {
+    GemmArgs ta = args;
+    ta.M = m_full;
+    const int gx = (N + 31) / 32, nb = gx * ((m_full - M + 31) / 32);
+    if (static_cast<int>(blockIdx.x) < nb) {
+      for (int t = static_cast<int>(blockIdx.x); t < nb; t += G) {
+        __syncthreads();  // every wave is past its last reads of the LDS that tail_block now fills
+        tail_block<EPI>(ta, M, t % gx, t / gx, smem);
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __syncthreads();  // the tail's LDS buffers overlap the ring's first slot
+    }
+  }
   if (total > 0) {
     issue();
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -888,16 +904,6 @@ __global__ __launch_bounds__(512, 1) void gemm_s8_persist_kernel(const GemmArgs 
     // live through the epilogue.
     read_frags(g, 0, 0);
     if (++r < my_tiles) coords(r, m0, n0);
-  }
-  // The rows M .. m_full - 1 past the whole row tiles, in 32 x 32 blocks over the grid (see tail_block).
-  if (m_full > M) {
-    GemmArgs ta = args;
-    ta.M = m_full;
-    const int gx = (N + 31) / 32, nb = gx * ((m_full - M + 31) / 32);
-    for (int t = static_cast<int>(blockIdx.x); t < nb; t += G) {
-      __syncthreads();  // every wave is past its last reads of the LDS that tail_block now fills
-      tail_block<EPI>(ta, M, t % gx, t / gx, smem);
-    }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
