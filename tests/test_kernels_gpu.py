@@ -147,7 +147,7 @@ def run_gemm(dev, a, w, rs, cs, bias, epi, variant, out=None, rope=None, q_scale
 
 
 GEMM_VARIANTS = [1, 2, 3, 4]  # ff_gemm_s8_variants()
-PERSISTENT = 4  # the persistent 256 x 256 variant (with its tail kernel for the rows past the last whole tile)
+PERSISTENT = 4  # the persistent 256 x 256 variant (with split-K blocks for the rows past the last whole tile)
 GEMM_SHAPES = [(1, 16, 64), (17, 48, 128), (300, 3072, 1024), (1025, 5632, 1024), (129, 1024, 2816), (257, 272, 192),
                (300, 1024, 2816)]
 
@@ -407,9 +407,9 @@ def test_empty_inputs_are_no_ops(dev):
     assert (r4 > 0).all()
 
 
-# The persistent variant sends the rows past its last whole 256-row tile to a split-K tail kernel (32 x 32 output
-# blocks, K in 128-byte chunks over 8 waves): tails of 1 .. 255 rows, a last column block of 16 columns, fewer K
-# chunks than waves and more.
+# The persistent variant computes the rows past its last whole 256-row tile as split-K blocks inside its launch,
+# before its tiles (32 x 32 output blocks, K in 128-byte chunks over 8 waves): tails of 1 .. 255 rows, a last column
+# block of 16 columns, fewer K chunks than waves and more, and more tail blocks than workgroups (767 x 5632).
 @pytest.mark.parametrize(("M", "N", "K"), [(511, 272, 384), (257, 96, 128), (288, 3072, 2816), (767, 5632, 1024)])
 def test_gemm_s8_tail_rows_int32_bit_exact(dev, rng, M, N, K):
     a, w, rs, cs, bias = gemm_inputs(rng, M, N, K)
