@@ -240,7 +240,7 @@ __global__ __launch_bounds__(256) void rot_q8_1024_kernel(const half_t* __restri
 // Rows are loaded at the top of their own iteration, not prefetched: the registers of a row in flight (8 NI per lane)
 // would cost occupancy, and more waves per SIMD hide the load better (at EVA02's 2816 columns, NI = 11, three waves
 // fit instead of two: 5-8 % faster; Haruka's rows 0-6 %).
-template <int NI, bool NORM, int G, bool FULL>
+template <int NI, bool NORM, int G, bool FULL, int TAIL>
 __global__ __launch_bounds__(256, NI > 8 ? 3 : 1) void rot_q8_h128_kernel(const half_t* __restrict__ x, int64_t T, int C, int c_real,
                                                           const float* __restrict__ gamma,
                                                           const float* __restrict__ beta, float eps,
@@ -272,6 +272,17 @@ __global__ __launch_bounds__(256, NI > 8 ? 3 : 1) void rot_q8_h128_kernel(const 
   // end get 0 from the same formula (c_real <= 128 nb).
   const int left0 = c_real - (g * 128 + 8 * gl);
   const float s3 = gray_sign(gl & 1), s4 = gray_sign(gl & 2), s5 = gray_sign(gl & 4), s6 = gray_sign(gl & 8);
+  // Block groups that can hold padding or lie past c_real: TAIL 2 none, 1 only the last one, 0 any (a uniform
+  // run-time test). With TAIL 1 or 2 the LayerNorm loop is straight-line code; the per-group branches of TAIL 0 cost
+  // 6-10 % at EVA02's 2816 columns and Haruka's 768 and 2048.
+  auto padded = [&](int i) __attribute__((always_inline)) {
+    if constexpr (TAIL == 2)
+      return false;
+    else if constexpr (TAIL == 1)
+      return i == NI - 1;
+    else
+      return (G * i + G) * 128 > c_real;
+  };
   auto tree_sum = [](float t) __attribute__((always_inline)) {
     if constexpr (G == 4) t = t + xor_shuffle(t, 32);
     t = t + swz_xor16(t);
@@ -292,10 +303,10 @@ __global__ __launch_bounds__(256, NI > 8 ? 3 : 1) void rot_q8_h128_kernel(const 
       return (e & 1) ? add_h<1>(w[i][e >> 1], s) : add_h<0>(w[i][e >> 1], s);
     };
     if constexpr (NORM) {
-      // Only block groups past column c_real - 128 G can hold padding or the row end (uniform test): the others skip
-      // the masks. The masked groups' counts come from one per-lane base re-read opaquely each row, so that the
-      // compiler neither hoists 8 NI loop-invariant lane masks into scalar registers nor holds NI counts in vector
-      // registers through the loop (at NI = 11 they spilled, and each reload waited for the row's loads).
+      // Only the padded() block groups can hold padding or the row end: the others skip the masks. The masked
+      // groups' counts come from one per-lane base re-read opaquely each row, so that the compiler neither hoists
+      // 8 NI loop-invariant lane masks into scalar registers nor holds NI counts in vector registers through the
+      // loop (at NI = 11 they spilled, and each reload waited for the row's loads).
       int lb = left0;
       asm volatile("" : "+v"(lb));
       int nr[NI];
@@ -304,7 +315,7 @@ __global__ __launch_bounds__(256, NI > 8 ? 3 : 1) void rot_q8_h128_kernel(const 
       float sum = 0.f;
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        if ((G * i + G) * 128 > c_real) {
+        if (padded(i)) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const float t = hv(i, e, sum);  // evaluated on every lane, then selected (no branch around the asm)
@@ -320,7 +331,7 @@ __global__ __launch_bounds__(256, NI > 8 ? 3 : 1) void rot_q8_h128_kernel(const 
       float sq = 0.f;
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        if ((G * i + G) * 128 > c_real) {
+        if (padded(i)) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const float t = hv(i, e, -mean);
@@ -343,7 +354,7 @@ __global__ __launch_bounds__(256, NI > 8 ? 3 : 1) void rot_q8_h128_kernel(const 
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         const int b = G * i + g;
-        if (b >= nb) continue;  // lanes past the row end keep zeros (they take part in the row's absmax)
+        if (!FULL && b >= nb) continue;  // lanes past the row end keep zeros (they take part in the row's absmax)
         const int c4 = (b * 128 + 8 * gl) >> 2;  // gamma/beta are zero past c_real: no masking inside the row
         const float4_t g0 = gbh[c4], g1 = gbh[c4 + 1], b0 = gbh[n4 + c4], b1 = gbh[n4 + c4 + 1];
 #pragma unroll
@@ -395,7 +406,7 @@ __global__ __launch_bounds__(256, NI > 8 ? 3 : 1) void rot_q8_h128_kernel(const 
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int b = G * i + g;
-      if (b < nb) {
+      if (FULL || b < nb) {
         uint2 pk;
         pk.x = pack4(v[i * 8] * mul, v[i * 8 + 1] * mul, v[i * 8 + 2] * mul, v[i * 8 + 3] * mul);
         pk.y = pack4(v[i * 8 + 4] * mul, v[i * 8 + 5] * mul, v[i * 8 + 6] * mul, v[i * 8 + 7] * mul);
@@ -417,19 +428,34 @@ static dim3 stride_grid(const void* kernel, size_t smem, int64_t T, int rows) {
 // 16-lane groups per row: 2 when the block count is even but not a multiple of 4 (768, 2816: no idle group), else 4
 static int h128_groups(int nb) { return nb % 2 == 0 && nb % 4 != 0 && nb / 2 <= 12 ? 2 : 4; }
 
+template <int NI, int G, bool FULL, int TAIL>
+static void launch_h128_norm(hipStream_t st, const half_t* x, int64_t T, int C, int c_real, const float* g,
+                             const float* b, float eps, int8_t* out, float* rs) {
+  const size_t smem = 2 * C * sizeof(float);
+  const dim3 grid = stride_grid(reinterpret_cast<const void*>(&rot_q8_h128_kernel<NI, true, G, FULL, TAIL>), smem, T,
+                                4 * (4 / G));
+  rot_q8_h128_kernel<NI, true, G, FULL, TAIL><<<grid, 256, smem, st>>>(x, T, C, c_real, g, b, eps, out, rs);
+}
 template <int NI, int G, bool FULL>
 static void launch_h128_rows(hipStream_t st, const half_t* x, int64_t T, int C, int c_real, const float* g,
                              const float* b, float eps, int8_t* out, float* rs) {
-  const int rows_per_block = 4 * (4 / G);
   if (g) {
-    const size_t smem = 2 * C * sizeof(float);
-    const dim3 grid = stride_grid(reinterpret_cast<const void*>(&rot_q8_h128_kernel<NI, true, G, FULL>), smem, T,
-                                  rows_per_block);
-    rot_q8_h128_kernel<NI, true, G, FULL><<<grid, 256, smem, st>>>(x, T, C, c_real, g, b, eps, out, rs);
+    // TAIL (see the kernel): whole rows of real columns need no masks, and when every block group but the last
+    // holds real columns only, only the last one does
+    if constexpr (FULL) {
+      if (c_real == C)
+        launch_h128_norm<NI, G, FULL, 2>(st, x, T, C, c_real, g, b, eps, out, rs);
+      else if (c_real >= (NI - 1) * G * 128)
+        launch_h128_norm<NI, G, FULL, 1>(st, x, T, C, c_real, g, b, eps, out, rs);
+      else
+        launch_h128_norm<NI, G, FULL, 0>(st, x, T, C, c_real, g, b, eps, out, rs);
+    } else {
+      launch_h128_norm<NI, G, FULL, 0>(st, x, T, C, c_real, g, b, eps, out, rs);
+    }
   } else {
-    const dim3 grid = stride_grid(reinterpret_cast<const void*>(&rot_q8_h128_kernel<NI, false, G, FULL>), 0, T,
-                                  rows_per_block);
-    rot_q8_h128_kernel<NI, false, G, FULL><<<grid, 256, 0, st>>>(x, T, C, c_real, g, b, eps, out, rs);
+    const dim3 grid = stride_grid(reinterpret_cast<const void*>(&rot_q8_h128_kernel<NI, false, G, FULL, 0>), 0, T,
+                                  4 * (4 / G));
+    rot_q8_h128_kernel<NI, false, G, FULL, 0><<<grid, 256, 0, st>>>(x, T, C, c_real, g, b, eps, out, rs);
   }
 }
 // FULL: the row's nb blocks fill all NI G lane groups, so every load is unconditional (straight-line loads let the

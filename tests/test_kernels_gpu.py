@@ -107,7 +107,8 @@ def test_rot_q8_h128_bit_exact(dev, rng, T, C):
     assert_codes_equal(run_h128(x, dev), OR.rot_q8_h128(x), f"h128 T={T} C={C}")
 
 
-@pytest.mark.parametrize(("C", "c_real"), [(2816, 2730), (768, 768), (2048, 2048), (1024, 1000), (4736, 4736), (256, 130)])
+@pytest.mark.parametrize(("C", "c_real"), [(2816, 2730), (768, 768), (2048, 2048), (1024, 1000), (4736, 4736), (256, 130),
+                                         (2816, 1000), (2048, 700), (4736, 4500)])
 def test_rot_q8_h128_layernorm_bit_exact(dev, rng, C, c_real):
     x = activations(rng, 257, C)
     x[:, c_real:] = 0
