@@ -193,6 +193,22 @@ def test_gemm_s8_epilogue_bit_exact(dev, rng, epi, variant):
     assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[:4].tolist()}: {got[tuple(bad[0])]} vs {want[tuple(bad[0])]}"
 
 
+@pytest.mark.parametrize("variant", GEMM_VARIANTS)
+@pytest.mark.parametrize("rope_len", [1, 5, 8, 65, 200])
+def test_gemm_s8_qkv_short_rope_tables(dev, rng, rope_len, variant):
+    # RoPE table row m % rope_len for tables shorter than a wave's rows (several wraps inside one output block), of a
+    # length below the rows per store pass (1, 5), equal to it (8) and odd; 600 rows leave a partial row tile and the
+    # persistent variant's split-K rows.
+    M, N, K = 600, 3072, 128
+    a, w, rs, cs, bias = gemm_inputs(rng, M, N, K)
+    cos = rng.uniform(-1, 1, (rope_len, 32)).astype(np.float32)
+    sin = rng.uniform(-1, 1, (rope_len, 32)).astype(np.float32)
+    got = run_gemm(dev, a, w, rs, cs, bias, OG.EPI_QKV_ROPE, variant, rope=(cos, sin), q_scale=OM.Q_SCALE)
+    want = OG.gemm_s8(a, w, rs, cs, bias, OG.EPI_QKV_ROPE, rope_cos=cos, rope_sin=sin, q_scale=OM.Q_SCALE)
+    bad = np.argwhere(got.view(np.uint16) != want.view(np.uint16))
+    assert bad.size == 0, f"rope_len {rope_len}: {len(bad)} mismatches, first at {bad[:4].tolist()}"
+
+
 # More 256 x 256 tiles than an MI355X holds workgroups (256): the persistent variant streams several tiles per
 # workgroup, its K ring running across tile boundaries, and takes the partial row tile last.
 MULTI_TILE_SHAPES = [(4100, 4096, 256), (32800, 1024, 128), (6000, 3072, 384)]
