@@ -89,8 +89,16 @@ __device__ __forceinline__ float silu(float g) {
   return g * __builtin_amdgcn_rcpf(1.f + e);
 }
 
+// The tanh GELU 0.5 y (1 + tanh(u)), u = sqrt(2/pi) (y + 0.044715 y^3), in the exactly equal form y / (1 + e^(-2u)),
+// from the hardware exp2 and reciprocal (each about 1 ulp): within a few fp32 ulp of the exact value for every y (the
+// form 0.5 y (1 + tanh(u)) cancels for negative y), where the reference itself evaluates tanh with a hardware
+// approximation (common.cuh:50-56); ~8 instructions instead of a library tanhf with branches. Limits: y -> -inf
+// gives e^(-2u) = inf, rcp = 0, gelu = -0; y -> +inf gives y.
 __device__ __forceinline__ float gelu_tanh(float y) {
-  return 0.5f * y * (1.f + tanhf(0.7978845608f * (y + 0.044715f * y * y * y)));
+  constexpr float K1 = -2.f * 1.4426950408889634f * 0.7978845608f;  // -2 sqrt(2/pi) log2(e)
+  constexpr float K3 = K1 * 0.044715f;
+  const float t = __builtin_fmaf(K3, y * y, K1) * y;  // -2u log2(e)
+  return y * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(t));
 }
 
 // Per-wave LDS staging area of store_epilogue: 32 rows of the wave's output columns, each row padded so that the
