@@ -75,6 +75,13 @@ __device__ __forceinline__ float add_h(uint32_t h2, float s) {
     asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(s));
   return r;
 }
+// 0 + the low half of h2 (a sum's first term, as the reference's sum starting from 0), with 0 an inline constant: a
+// register operand holding 0 would be hoisted out of the row loop and hold a register through it.
+__device__ __forceinline__ float add_h_zero(uint32_t h2) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, 1.0, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2));
+  return r;
+}
 __device__ __forceinline__ void bfly0_h(uint32_t h2, float& lo_plus_hi, float& lo_minus_hi) {
   asm("v_fma_mix_f32 %0, %1, 1.0, %1 op_sel:[0,0,1] op_sel_hi:[1,0,1]" : "=v"(lo_plus_hi) : "v"(h2));
   asm("v_fma_mix_f32 %0, %1, -1.0, %1 op_sel:[1,0,0] op_sel_hi:[1,0,1]" : "=v"(lo_minus_hi) : "v"(h2));
@@ -268,9 +275,6 @@ __global__ __launch_bounds__(256, NI > 8 ? 3 : 1) void rot_q8_h128_kernel(const 
       nxt[i] = (FULL || b < nb) ? *reinterpret_cast<const half8_t*>(x + r * C + b * 128 + 8 * gl) : half8_t{};
     }
   };
-  // Real columns among the lane's 8 of block G i + g (a prefix): clamp(left0 - 128 G i, 0, 8). Blocks past the row
-  // end get 0 from the same formula (c_real <= 128 nb).
-  const int left0 = c_real - (g * 128 + 8 * gl);
   const float s3 = gray_sign(gl & 1), s4 = gray_sign(gl & 2), s5 = gray_sign(gl & 4), s6 = gray_sign(gl & 8);
   // Block groups that can hold padding or lie past c_real: TAIL 2 none, 1 only the last one, 0 any (a uniform
   // run-time test). With TAIL 1 or 2 the LayerNorm loop is straight-line code; the per-group branches of TAIL 0 cost
@@ -303,12 +307,17 @@ __global__ __launch_bounds__(256, NI > 8 ? 3 : 1) void rot_q8_h128_kernel(const 
       return (e & 1) ? add_h<1>(w[i][e >> 1], s) : add_h<0>(w[i][e >> 1], s);
     };
     if constexpr (NORM) {
-      // Only the padded() block groups can hold padding or the row end: the others skip the masks. The masked
-      // groups' counts come from one per-lane base re-read opaquely each row, so that the compiler neither hoists
-      // 8 NI loop-invariant lane masks into scalar registers nor holds NI counts in vector registers through the
-      // loop (at NI = 11 they spilled, and each reload waited for the row's loads).
-      int lb = left0;
-      asm volatile("" : "+v"(lb));
+      // Only the padded() block groups can hold padding or the row end: the others skip the masks. Real columns
+      // among the lane's 8 of block G i + g (a prefix): clamp(lb - 128 G i, 0, 8), with lb = c_real minus the lane's
+      // first column of block g; blocks past the row end get 0 from the same formula (c_real <= 128 nb). lb is
+      // recomputed each row from an opaque copy of the lane index (a few VALU), so that the compiler neither hoists
+      // 8 NI loop-invariant lane masks into scalar registers nor holds counts through the loop: held, at NI = 11
+      // they spilled, and a spill reload, queued behind the row's loads in the in-order memory counter, made the
+      // wave wait for nearly the whole row before its first add.
+      int ln = static_cast<int>(threadIdx.x);
+      asm volatile("" : "+v"(ln));
+      const int ls = ln & 15;
+      const int lb = c_real - (((ln >> 4) & (G - 1)) * 128 + 8 * (ls ^ (ls >> 1)));
       int nr[NI];
 #pragma unroll
       for (int i = 0; i < NI; ++i) nr[i] = min(max(lb - 128 * G * i, 0), 8);
@@ -318,12 +327,13 @@ __global__ __launch_bounds__(256, NI > 8 ? 3 : 1) void rot_q8_h128_kernel(const 
         if (padded(i)) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const float t = hv(i, e, sum);  // evaluated on every lane, then selected (no branch around the asm)
+            // evaluated on every lane, then selected (no branch around the asm)
+            const float t = i == 0 && e == 0 ? add_h_zero(w[0][0]) : hv(i, e, sum);
             sum = e < nr[i] ? t : sum;
           }
         } else {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) sum = hv(i, e, sum);
+          for (int e = 0; e < 8; ++e) sum = i == 0 && e == 0 ? add_h_zero(w[0][0]) : hv(i, e, sum);
         }
       }
       const float fr = static_cast<float>(c_real);
