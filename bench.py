@@ -65,48 +65,76 @@ def timed(fn, stream, iters=20, warm=3) -> float:
     return s.elapsed_time(e) / iters * 1e3
 
 
+def in_forward_order(seq, stream, reps: int = 2) -> dict:
+    """Average duration (us) per kernel name of `seq`, the (name, launch) pairs of one forward's blocks in forward
+    order, each timed between HIP events recorded on the stream the kernels run on, one event after every launch
+    (an event adds ~2 us to the launch it follows). Timed in sequence, not each kernel on its own: repeated launches
+    of one kernel find its operands in the caches, and a rotation then runs up to ~15 % faster than inside the
+    forward. The first pass over `seq` is a warm-up."""
+    import torch
+
+    for _, fn in seq:
+        fn()
+    acc: dict[str, list[float]] = {}
+    for _ in range(reps):
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(len(seq) + 1)]
+        torch.cuda.synchronize()
+        evs[0].record(stream)
+        for i, (_, fn) in enumerate(seq):
+            fn()
+            evs[i + 1].record(stream)
+        torch.cuda.synchronize()
+        for i, (name, _) in enumerate(seq):
+            acc.setdefault(name, []).append(evs[i].elapsed_time(evs[i + 1]) * 1e3)
+    return {name: sum(v) / len(v) for name, v in acc.items()}
+
+
+def kernel_row(us: float, bound: str, work: int, per_fwd: int) -> dict:
+    if bound == "hbm":
+        ach, peak, unit = work / us / 1e3, PEAK_HBM_GBS, "GB/s"
+    elif bound == "mfma_int8":
+        ach, peak, unit = work / us / 1e6, PEAK_INT8_TOPS, "TOP/s"
+    else:
+        ach, peak, unit = work / us / 1e6, PEAK_FP16_TFLOPS, "TFLOP/s"
+    return {"us": round(us, 2), "launches_per_step": per_fwd, "work_per_launch": work, "achieved": round(ach, 1),
+            "unit": unit, "peak": peak, "frac": round(ach / peak, 4), "bound": "hbm" if bound == "hbm" else "mfma"}
+
+
 def kernel_table(eng, B: int, buf) -> dict:
-    """Each block kernel timed in isolation on the graph's buffers; algorithmic work per launch and roofline."""
+    """The block kernels of a whole forward (every layer's weights) run in forward order on the graph's buffers,
+    each launch timed (in_forward_order); algorithmic work per launch and roofline per kernel."""
     import torch
 
     from foidfinder_amd.kernels import EPI_QKV_ROPE, EPI_RESIDUAL, EPI_SWIGLU
 
-    cfg, k, lw = eng.cfg, eng.k, eng.layers[0]
-    M, d, h, hp = B * cfg.tokens, cfg.dim, cfg.hidden, cfg.hidden_pad
-    st = torch.cuda.current_stream()
+    cfg, k = eng.cfg, eng.k
+    M, d, h, hp, L, eps = B * cfg.tokens, cfg.dim, cfg.hidden, cfg.hidden_pad, cfg.tokens, cfg.eps
     v = {n: eng.variants.get((n, B), 0) for n in ("qkv", "proj", "fc1", "fc2")}
-    x2 = buf["x"].clone()  # residual epilogues write into a scratch copy
-    jobs = {
-        "rot_q8_1024_ln": (lambda: k.rot_q8_1024(buf["x"], *lw["n1"], buf["a8"], buf["rs"], cfg.eps),
-                           "hbm", M * d * 2 + M * d + 4 * M + 8 * d, 2 * cfg.depth),
-        "rot_q8_1024": (lambda: k.rot_q8_1024(buf["o16"], None, None, buf["a8"], buf["rs"], cfg.eps),
-                        "hbm", M * d * 3 + 4 * M, cfg.depth),
-        "rot_q8_h128_ln": (lambda: k.rot_q8_h128(buf["h16"], buf["h8"], buf["rs"], *lw["nm"], h, cfg.eps),
-                           "hbm", M * hp * 3 + 4 * M + 8 * h, cfg.depth),
-        "gemm_qkv": (lambda: eng._gemm(buf["a8"], lw["qkv"], buf["rs"], EPI_QKV_ROPE, v["qkv"], buf["qkv"], eng.rope),
-                     "mfma_int8", 2 * M * 3 * d * d, cfg.depth),
-        "gemm_proj": (lambda: eng._gemm(buf["a8"], lw["proj"], buf["rs"], EPI_RESIDUAL, v["proj"], x2),
-                      "mfma_int8", 2 * M * d * d, cfg.depth),
-        "gemm_fc1": (lambda: eng._gemm(buf["a8"], lw["fc1"], buf["rs"], EPI_SWIGLU, v["fc1"], buf["h16"]),
-                     "mfma_int8", 2 * M * 2 * h * d, cfg.depth),
-        "gemm_fc2": (lambda: eng._gemm(buf["h8"], lw["fc2"], buf["rs"], EPI_RESIDUAL, v["fc2"], x2),
-                     "mfma_int8", 2 * M * d * h, cfg.depth),
-        "attention": (lambda: k.attention(buf["qkv"], buf["o16"], cfg.tokens),
-                      "mfma_fp16", 4 * B * cfg.heads * cfg.tokens * cfg.tokens * 64, cfg.depth),
+    x, a8, rs = buf["x"], buf["a8"], buf["rs"]
+    meta = {
+        "rot_q8_1024_ln": ("hbm", M * d * 2 + M * d + 4 * M + 8 * d, 2 * cfg.depth),
+        "rot_q8_1024": ("hbm", M * d * 3 + 4 * M, cfg.depth),
+        "rot_q8_h128_ln": ("hbm", M * hp * 3 + 4 * M + 8 * h, cfg.depth),
+        "gemm_qkv": ("mfma_int8", 2 * M * 3 * d * d, cfg.depth),
+        "gemm_proj": ("mfma_int8", 2 * M * d * d, cfg.depth),
+        "gemm_fc1": ("mfma_int8", 2 * M * 2 * h * d, cfg.depth),
+        "gemm_fc2": ("mfma_int8", 2 * M * d * h, cfg.depth),
+        "attention": ("mfma_fp16", 4 * B * cfg.heads * L * L * 64, cfg.depth),
     }
-    out = {}
-    for name, (fn, bound, work, per_fwd) in jobs.items():
-        us = timed(fn, st)
-        if bound == "hbm":
-            ach, peak, unit = work / us / 1e3, PEAK_HBM_GBS, "GB/s"
-        elif bound == "mfma_int8":
-            ach, peak, unit = work / us / 1e6, PEAK_INT8_TOPS, "TOP/s"
-        else:
-            ach, peak, unit = work / us / 1e6, PEAK_FP16_TFLOPS, "TFLOP/s"
-        out[name] = {"us": round(us, 2), "launches_per_step": per_fwd, "work_per_launch": work,
-                     "achieved": round(ach, 1), "unit": unit, "peak": peak, "frac": round(ach / peak, 4),
-                     "bound": "hbm" if bound == "hbm" else "mfma"}
-    return out
+
+    def block(lw):  # Eva02Int8._forward's block, kernel by kernel
+        return [("rot_q8_1024_ln", lambda: k.rot_q8_1024(x, *lw["n1"], a8, rs, eps)),
+                ("gemm_qkv", lambda: eng._gemm(a8, lw["qkv"], rs, EPI_QKV_ROPE, v["qkv"], buf["qkv"], eng.rope)),
+                ("attention", lambda: k.attention(buf["qkv"], buf["o16"], L)),
+                ("rot_q8_1024", lambda: k.rot_q8_1024(buf["o16"], None, None, a8, rs, eps)),
+                ("gemm_proj", lambda: eng._gemm(a8, lw["proj"], rs, EPI_RESIDUAL, v["proj"], x)),
+                ("rot_q8_1024_ln", lambda: k.rot_q8_1024(x, *lw["n2"], a8, rs, eps)),
+                ("gemm_fc1", lambda: eng._gemm(a8, lw["fc1"], rs, EPI_SWIGLU, v["fc1"], buf["h16"])),
+                ("rot_q8_h128_ln", lambda: k.rot_q8_h128(buf["h16"], buf["h8"], rs, *lw["nm"], h, eps)),
+                ("gemm_fc2", lambda: eng._gemm(buf["h8"], lw["fc2"], rs, EPI_RESIDUAL, v["fc2"], x))]
+
+    us = in_forward_order([job for lw in eng.layers for job in block(lw)], torch.cuda.current_stream())
+    return {name: kernel_row(us[name], *meta[name]) for name in meta}
 
 
 def cpu_threads() -> int:
@@ -257,17 +285,6 @@ def bench_pixai(args) -> None:
     print(json.dumps(line), flush=True)
 
 
-def kernel_row(us: float, bound: str, work: int, per_fwd: int) -> dict:
-    if bound == "hbm":
-        ach, peak, unit = work / us / 1e3, PEAK_HBM_GBS, "GB/s"
-    elif bound == "mfma_int8":
-        ach, peak, unit = work / us / 1e6, PEAK_INT8_TOPS, "TOP/s"
-    else:
-        ach, peak, unit = work / us / 1e6, PEAK_FP16_TFLOPS, "TFLOP/s"
-    return {"us": round(us, 2), "launches_per_step": per_fwd, "work_per_launch": work, "achieved": round(ach, 1),
-            "unit": unit, "peak": peak, "frac": round(ach / peak, 4), "bound": "hbm" if bound == "hbm" else "mfma"}
-
-
 def bench_haruka(args) -> None:
     """Haruka Tagger (EVA02-B/14 at 448 px, 12 int8 blocks of d 768, tree pool, 1152 -> 98782 head), random-init
     weights in the reference's folded format, converted to int8 on load: graph-replay time per batch (raw uint8
@@ -309,32 +326,37 @@ def bench_haruka(args) -> None:
     print(f"{ips:.1f} images/s, {ms:.2f} ms per batch of {B}", file=sys.stderr, flush=True)
 
     buf = eng._graphs[B][3]
-    k, lw, st = eng.k, eng.layers[0], torch.cuda.current_stream()
-    M, d, h, L = B * cfg.tokens, cfg.dim, cfg.hidden, cfg.tokens
+    k, st = eng.k, torch.cuda.current_stream()
+    M, d, h, L, eps = B * cfg.tokens, cfg.dim, cfg.hidden, cfg.tokens, cfg.eps
     v = {n: eng.variants.get((n, B), 0) for n in ("qkv", "proj", "fc1", "fc2")}
-    x2 = buf["x"].clone()
-    jobs = {
-        "rot_q8_h128_ln_768": (lambda: k.rot_q8_h128(buf["x"], buf["a8"], buf["rs"], *lw["n1"], d, cfg.eps),
-                               "hbm", M * d * 3 + 4 * M + 8 * d, 2 * cfg.depth),
-        "rot_q8_h128_768": (lambda: k.rot_q8_h128(buf["o16"], buf["a8"], buf["rs"]), "hbm", M * d * 3 + 4 * M,
-                            cfg.depth),
-        "rot_q8_h128_ln_2048": (lambda: k.rot_q8_h128(buf["h16"], buf["h8"], buf["rs"], *lw["nm"], h, cfg.eps),
-                                "hbm", M * h * 3 + 4 * M + 8 * h, cfg.depth),
-        "gemm_qkv": (lambda: eng._gemm(buf["a8"], lw["qkv"], buf["rs"], EPI_QKV_ROPE, v["qkv"], buf["qkv"], eng.rope),
-                     "mfma_int8", 2 * M * 3 * d * d, cfg.depth),
-        "gemm_proj": (lambda: eng._gemm(buf["a8"], lw["proj"], buf["rs"], EPI_RESIDUAL, v["proj"], x2),
-                      "mfma_int8", 2 * M * d * d, cfg.depth),
-        "gemm_fc1": (lambda: eng._gemm(buf["a8"], lw["fc1"], buf["rs"], EPI_SWIGLU, v["fc1"], buf["h16"]),
-                     "mfma_int8", 2 * M * 2 * h * d, cfg.depth),
-        "gemm_fc2": (lambda: eng._gemm(buf["h8"], lw["fc2"], buf["rs"], EPI_RESIDUAL, v["fc2"], x2),
-                     "mfma_int8", 2 * M * d * h, cfg.depth),
-        "attention": (lambda: k.attention(buf["qkv"], buf["o16"], L), "mfma_fp16", 4 * B * cfg.heads * L * L * 64,
-                      cfg.depth),
-        # the head GEMM's fp16 weights dominate the pool head's bytes
-        "pool_head": (lambda: eng.pool_head(buf["x"].view(B, L, d)), "hbm",
-                      cfg.tags * cfg.leaves * cfg.leaf_dim * 2, 1),
+    x, a8, rs = buf["x"], buf["a8"], buf["rs"]
+    meta = {
+        "rot_q8_h128_ln_768": ("hbm", M * d * 3 + 4 * M + 8 * d, 2 * cfg.depth),
+        "rot_q8_h128_768": ("hbm", M * d * 3 + 4 * M, cfg.depth),
+        "rot_q8_h128_ln_2048": ("hbm", M * h * 3 + 4 * M + 8 * h, cfg.depth),
+        "gemm_qkv": ("mfma_int8", 2 * M * 3 * d * d, cfg.depth),
+        "gemm_proj": ("mfma_int8", 2 * M * d * d, cfg.depth),
+        "gemm_fc1": ("mfma_int8", 2 * M * 2 * h * d, cfg.depth),
+        "gemm_fc2": ("mfma_int8", 2 * M * d * h, cfg.depth),
+        "attention": ("mfma_fp16", 4 * B * cfg.heads * L * L * 64, cfg.depth),
     }
-    kern = {name: kernel_row(timed(fn, st), bound, work, n) for name, (fn, bound, work, n) in jobs.items()}
+
+    def block(lw):  # HarukaInt8._forward's block, kernel by kernel
+        return [("rot_q8_h128_ln_768", lambda: k.rot_q8_h128(x, a8, rs, *lw["n1"], d, eps)),
+                ("gemm_qkv", lambda: eng._gemm(a8, lw["qkv"], rs, EPI_QKV_ROPE, v["qkv"], buf["qkv"], eng.rope)),
+                ("attention", lambda: k.attention(buf["qkv"], buf["o16"], L)),
+                ("rot_q8_h128_768", lambda: k.rot_q8_h128(buf["o16"], a8, rs)),
+                ("gemm_proj", lambda: eng._gemm(a8, lw["proj"], rs, EPI_RESIDUAL, v["proj"], x)),
+                ("rot_q8_h128_ln_768", lambda: k.rot_q8_h128(x, a8, rs, *lw["n2"], d, eps)),
+                ("gemm_fc1", lambda: eng._gemm(a8, lw["fc1"], rs, EPI_SWIGLU, v["fc1"], buf["h16"])),
+                ("rot_q8_h128_ln_2048", lambda: k.rot_q8_h128(buf["h16"], buf["h8"], rs, *lw["nm"], h, eps)),
+                ("gemm_fc2", lambda: eng._gemm(buf["h8"], lw["fc2"], rs, EPI_RESIDUAL, v["fc2"], x))]
+
+    us = in_forward_order([job for lw in eng.layers for job in block(lw)], st)
+    kern = {name: kernel_row(us[name], *m) for name, m in meta.items()}
+    # the pool head (the head GEMM's fp16 weights dominate its bytes), eager: its ~40 launches time on their own
+    kern["pool_head"] = kernel_row(timed(lambda: eng.pool_head(x.view(B, L, d)), st), "hbm",
+                                   cfg.tags * cfg.leaves * cfg.leaf_dim * 2, 1)
     for n, r in kern.items():
         print(f"  {n:20s} {r['us']:8.1f} us x{r['launches_per_step']:3d}  {r['achieved']:8.1f} {r['unit']}"
               f"  ({100 * r['frac']:.1f}% of peak)", file=sys.stderr, flush=True)
@@ -375,6 +397,8 @@ def bench_haruka(args) -> None:
         "roofline": {"kernel": dom, **{f: kern[dom][f] for f in ("bound", "achieved", "peak", "frac")},
                      "unit": "GB/s" if kern[dom]["unit"] == "GB/s" else "TFLOP/s"},
         "kernels": kern,
+        "kernel_timing": "block kernels of one forward in forward order, 2 passes, a HIP event after each launch "
+                         "(~2 us per event included); pool_head eager, 20 calls",
         "gemm_variants": v,
         "work_per_step": {"gemm_int8_ops": sum(cfg.gemm_ops(B).values()), "attention_flops": cfg.attention_flops(B)},
     }
@@ -468,6 +492,8 @@ def main():
                      # the roofline object's unit is "GB/s" or "TFLOP/s"; int8 rates are tera-ops (2 per multiply-add)
                      "unit": "GB/s" if dk["unit"] == "GB/s" else "TFLOP/s", "frac": dk["frac"], "traffic": traffic},
         "kernels": kern,
+        "kernel_timing": "one forward's block kernels in forward order, 2 passes, a HIP event after each launch "
+                         "(~2 us per event included)",
         "gemm_variants": {name: eng.variants.get((name, B), 0) for name in ("qkv", "proj", "fc1", "fc2")},
         "cpu_baseline": cpu,
     }
