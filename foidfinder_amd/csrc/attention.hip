@@ -29,7 +29,9 @@
 // the last tile's second half holds no key below L it is skipped. The last query block of a sequence, when it holds
 // two 32-query units, gives each unit two waves, one per key half; when it holds one (L = 1025 leaves one query), all
 // four waves share it, each over one key half of every other tile. The partial results are merged through LDS at the
-// end, so that block takes about a quarter of a block's time instead of a whole block's with three waves idle.
+// end, so that block takes about a quarter of a block's time instead of a whole block's with three waves idle. A grid
+// of 128-query blocks that does not fill the GPU's resident workgroups once (small batches, PixAI's 576-token
+// windows) runs as 64-query blocks instead, each unit split over two waves by key half: twice the workgroups.
 //
 // Reference: foidfinder/backends/cuda/csrc/attention.cuh:19-157 (which accumulates each 64-key block in fp16 and
 // rescales every block; here every product and sum is fp32).
@@ -70,13 +72,14 @@ __device__ __forceinline__ void tr_read(half4_t& v, uint32_t lds_addr) {
   asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(lds_addr), "n"(OFF) : "memory");
 }
 
-// One workgroup's work. SPLIT = 0: wave w owns queries qb*BQ + 32w .. +31 over both key halves of every tile.
+// One workgroup's work, the queries from q_first. SPLIT = 0: wave w owns queries q_first + 32w .. +31 over both
+// key halves of every tile.
 // SPLIT = 1 (last block of two units): waves 2u and 2u + 1 share query unit u, each over one key half (kh_sel = w & 1);
 // the half-1 wave's O, m_ref and l are merged into its partner's at the end. SPLIT = 2 (last block of one unit): all
 // four waves share unit 0, wave w over key half w & 1 of the tiles of parity w >> 1; waves 1-3 are merged into wave 0.
 template <int SPLIT>
 __device__ __forceinline__ void attention_block(const half_t* __restrict__ qkv, half_t* __restrict__ out, int L,
-                                                int H, int qb, int h, int seq, half_t* smem) {
+                                                int H, int q_first, int h, int seq, half_t* smem) {
   const uint32_t smem_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)smem));
   const int C = H * HD, ROW = 3 * C;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -90,7 +93,7 @@ __device__ __forceinline__ void attention_block(const half_t* __restrict__ qkv, 
   const int kh_sel = SPLIT ? wave & 1 : 0;
   const int first_tile = SPLIT == 2 ? wave >> 1 : 0;  // SPLIT 2: the wave computes tiles first_tile, +2, ...
   bool seen = false;                                   // the wave has computed a tile (it has keys to merge)
-  const int q0 = qb * BQ + unit * QW;
+  const int q0 = q_first + unit * QW;
   const bool active = q0 < L;  // a wave whose queries all lie past L only helps load K and V
   const int ntiles = (L + BKV - 1) / BKV;
   const bool h1_empty = (ntiles - 1) * BKV + 32 >= L;  // the last tile's keys 32..63 all lie past L
@@ -391,22 +394,25 @@ __device__ __forceinline__ void attention_block(const half_t* __restrict__ qkv, 
   }
 }
 
+// bq: queries per workgroup, BQ (one 32-query unit per wave) or BQ / 2 (two units, each split over two waves by key
+// half: twice the workgroups for grids that do not fill the GPU once).
 __global__ __launch_bounds__(64 * WAVES, 4) void attention_kernel(const half_t* __restrict__ qkv,
-                                                                  half_t* __restrict__ out, int L, int H) {
+                                                                  half_t* __restrict__ out, int L, int H, int bq) {
   // K tile of ring slot st at smem + st*TILE, V tile at smem + (STAGES + st)*TILE
   __shared__ __attribute__((aligned(1024))) half_t smem[2 * STAGES * TILE];
   // 1-D grid over (sequence, head, query block), query block fastest, remapped so that all query blocks of one
   // (sequence, head) run on one XCD and read its K and V through one L2.
-  const int nq = (L + BQ - 1) / BQ;
+  const int nq = (L + bq - 1) / bq;
   const int t = xcd_remap(blockIdx.x, gridDim.x);
   const int qb = t % nq, h = (t / nq) % H, seq = t / (nq * H);
-  const int units = min(WAVES, (L - qb * BQ + QW - 1) / QW);  // 32-query units of this block
+  const int q_first = qb * bq;
+  const int units = min(bq / QW, (L - q_first + QW - 1) / QW);  // 32-query units of this block
   if (units == 1)
-    attention_block<2>(qkv, out, L, H, qb, h, seq, smem);
+    attention_block<2>(qkv, out, L, H, q_first, h, seq, smem);
   else if (2 * units <= WAVES)
-    attention_block<1>(qkv, out, L, H, qb, h, seq, smem);
+    attention_block<1>(qkv, out, L, H, q_first, h, seq, smem);
   else
-    attention_block<0>(qkv, out, L, H, qb, h, seq, smem);
+    attention_block<0>(qkv, out, L, H, q_first, h, seq, smem);
 }
 
 }  // namespace ff
@@ -425,11 +431,16 @@ extern "C" int ff_attention(const void* qkv, void* out, int64_t T, int64_t heads
   if (!qkv || !out) return fail(FF_EINVAL, "attention: null pointer");
   if ((reinterpret_cast<uintptr_t>(qkv) & 15) || (reinterpret_cast<uintptr_t>(out) & 7))
     return fail(FF_EINVAL, "attention: misaligned pointer");
-  const int64_t blocks = (seq_len + BQ - 1) / BQ * heads * seqs;
+  // 128-query blocks; when they do not fill the GPU's resident workgroups once, 64-query blocks (twice as many)
+  int64_t resident = resident_blocks(reinterpret_cast<const void*>(&attention_kernel), 64 * WAVES, 0);
+  if (resident <= 0) resident = 1024;
+  const int64_t blocks_full = (seq_len + BQ - 1) / BQ * heads * seqs;
+  const int bq = blocks_full < resident ? BQ / 2 : BQ;
+  const int64_t blocks = (seq_len + bq - 1) / bq * heads * seqs;
   if (blocks > 0x7fffffff) return fail(FF_EINVAL, "attention: too many blocks");
   const dim3 grid(static_cast<unsigned>(blocks));
   attention_kernel<<<grid, 64 * WAVES, 0, as_stream(stream)>>>(static_cast<const half_t*>(qkv),
                                                                 static_cast<half_t*>(out), static_cast<int>(seq_len),
-                                                                static_cast<int>(heads));
+                                                                static_cast<int>(heads), bq);
   return check_launch("attention");
 }

@@ -343,6 +343,17 @@ def test_attention_split_tail_blocks(dev, rng, S, L, H):
     check_attention(got, want, H)
 
 
+# The cases above launch fewer 128-query blocks than an MI355X holds resident, so they run as 64-query blocks (each
+# 32-query unit over two waves by key half). These grids (2048 and 1728 blocks of 128 queries) run as 128-query blocks,
+# one unit per wave, with the split tail blocks at their ends.
+@pytest.mark.parametrize(("S", "L", "H"), [(64, 161, 16), (12, 1025, 16)])
+def test_attention_full_blocks_on_large_grids(dev, rng, S, L, H):
+    qkv = qkv_inputs(rng, S, L, H)
+    got = run_attention(dev, qkv, L).astype(np.float64)
+    want = OA.attention(qkv, L, out_dtype=np.float64)
+    check_attention(got, want, H)
+
+
 @pytest.mark.parametrize(("gain", "ramp"), [(8.0, 3.0), (30.0, 0.0), (4.0, 12.0)])
 def test_attention_peaked_and_rising_scores(dev, rng, gain, ramp):
     """Scores of tens to hundreds (base 2) whose maxima grow along the keys: the running maximum must be raised on
