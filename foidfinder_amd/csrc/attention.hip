@@ -30,8 +30,8 @@
 // two 32-query units, gives each unit two waves, one per key half; when it holds one (L = 1025 leaves one query), all
 // four waves share it, each over one key half of every other tile. The partial results are merged through LDS at the
 // end, so that block takes about a quarter of a block's time instead of a whole block's with three waves idle. A grid
-// of 128-query blocks that does not fill the GPU's resident workgroups once (small batches, PixAI's 576-token
-// windows) runs as 64-query blocks instead, each unit split over two waves by key half: twice the workgroups.
+// of 128-query blocks that fills at most half of the GPU's resident workgroups (batch 1 and 2) runs as 64-query blocks
+// instead, each unit over two waves by key half: twice the workgroups.
 //
 // Reference: foidfinder/backends/cuda/csrc/attention.cuh:19-157 (which accumulates each 64-key block in fp16 and
 // rescales every block; here every product and sum is fp32).
@@ -394,8 +394,8 @@ __device__ __forceinline__ void attention_block(const half_t* __restrict__ qkv, 
   }
 }
 
-// bq: queries per workgroup, BQ (one 32-query unit per wave) or BQ / 2 (two units, each split over two waves by key
-// half: twice the workgroups for grids that do not fill the GPU once).
+// bq: queries per workgroup, BQ (one 32-query unit per wave) or BQ / 2 (two units, each over two waves by key half:
+// twice the workgroups for grids far from filling the GPU once).
 __global__ __launch_bounds__(64 * WAVES, 4) void attention_kernel(const half_t* __restrict__ qkv,
                                                                   half_t* __restrict__ out, int L, int H, int bq) {
   // K tile of ring slot st at smem + st*TILE, V tile at smem + (STAGES + st)*TILE
@@ -431,11 +431,12 @@ extern "C" int ff_attention(const void* qkv, void* out, int64_t T, int64_t heads
   if (!qkv || !out) return fail(FF_EINVAL, "attention: null pointer");
   if ((reinterpret_cast<uintptr_t>(qkv) & 15) || (reinterpret_cast<uintptr_t>(out) & 7))
     return fail(FF_EINVAL, "attention: misaligned pointer");
-  // 128-query blocks; when they do not fill the GPU's resident workgroups once, 64-query blocks (twice as many)
+  // 128-query blocks; 64-query blocks (twice as many) when those still fit the GPU's resident workgroups at once.
+  // Measured: EVA02-L at batch 1 (144 -> 288 blocks) 16.4 -> 15.1 us; grids that the halving pushes past one round
+  // run slower (PixAI's windows, 720 -> 1296 blocks: 23.9 -> 27.3 us), and so did 32-query blocks at batch 1.
   int64_t resident = resident_blocks(reinterpret_cast<const void*>(&attention_kernel), 64 * WAVES, 0);
   if (resident <= 0) resident = 1024;
-  const int64_t blocks_full = (seq_len + BQ - 1) / BQ * heads * seqs;
-  const int bq = blocks_full < resident ? BQ / 2 : BQ;
+  const int bq = (seq_len + BQ / 2 - 1) / (BQ / 2) * heads * seqs <= resident ? BQ / 2 : BQ;
   const int64_t blocks = (seq_len + bq - 1) / bq * heads * seqs;
   if (blocks > 0x7fffffff) return fail(FF_EINVAL, "attention: too many blocks");
   const dim3 grid(static_cast<unsigned>(blocks));
