@@ -261,8 +261,9 @@ class PixAIInt8(Int8Engine):
         """x fp16 [B, tokens, d] -> logits fp32 [B, tags] (reference.py:133-140).
 
         The attention of one learned query per head over the tokens is a matrix-vector product, a softmax and a
-        weighted sum, done here in fp32 on the fp16 keys and values (the reference's scaled_dot_product_attention
-        of a single query: its fused kernel took 143 us per image at 1008 px for ~21 MB of keys and values)."""
+        weighted sum, done here in fp32 on the fp16 keys and values, instead of the reference's
+        scaled_dot_product_attention of a single query (at 1008 px the stem, pool head and classifier took 316 us
+        per image with it and 249 us this way, by kernel traces of one forward)."""
         cfg = self.cfg
         B, L, d, H = x.shape[0], cfg.tokens, cfg.dim, cfg.heads
         h = F.layer_norm(x, (d,), *self.pool_norm, cfg.eps) + self.pool_pos
