@@ -142,55 +142,86 @@ __global__ __launch_bounds__(256) void layer_norm2_vec_kernel(const half_t* __re
 // Tokens per workgroup of slot_weights.
 constexpr int SW_TOKENS = 32;
 
-// Grid (token blocks of 32, batch). Thread t handles pairs (token, head) p = t, t + 256, ... of the block's 32 x G:
-// it reads the pair's M logits (+ c, the queries' key-bias terms), computes the weights in fp32 and puts them into an
-// LDS tile [G*M][32] (transposed); the tile is then written out row by row (32 contiguous tokens per query column,
-// two columns per wave), and each column's fp32 sum over the block's tokens goes to partial[b, block, column].
+// Grid (token blocks of 32, batch). The block's logits [ntok][G*M] are one contiguous run: the workgroup first copies
+// them into LDS (16-byte loads when G*M % 8 == 0 and the base is 16-byte aligned, else 2-byte ones). Thread t then
+// handles pairs (token, head) p = t, t + 256, ... of the block's 32 x G: it reads the pair's M logits (+ c, the
+// queries' key-bias terms) from LDS and computes the weights in fp32 from the hardware exp2 and reciprocal (each about
+// 1 ulp), softmax over the queries times sigmoid(logit + bias), keeping them in registers. After a barrier the same
+// LDS holds the weights as a tile [G*M][32] (transposed), which is written out row by row (32 contiguous tokens per
+// query column, two columns per wave); each column's fp32 sum over the block's tokens goes to partial[b, block,
+// column] (summed in token order by one thread per column). PMAX bounds the pairs per thread: the host allows G*M <= 496, i.e. 32 G <= 256 PMAX.
 template <int M>
 __global__ __launch_bounds__(256) void slot_weights_kernel(const half_t* __restrict__ logits, const float* __restrict__ c,
                                                            int64_t c_stride, const float* __restrict__ bias, int N,
-                                                           int G, half_t* __restrict__ a_t,
+                                                           int G, int vec, half_t* __restrict__ a_t,
                                                            float* __restrict__ partial) {
-  extern __shared__ float tile[];  // [G*M][SW_TOKENS + 1] fp32 weights
+  constexpr int PMAX = M == 18 ? 4 : 8;
+  constexpr float LOG2E = 1.4426950408889634f;
+  extern __shared__ float tile[];  // first the logits block (fp16), then [G*M][SW_TOKENS + 1] fp32 weights
+  half_t* lh = reinterpret_cast<half_t*>(tile);
   const int GM = G * M, b = blockIdx.y, n0 = blockIdx.x * SW_TOKENS;
   const int ntok = min(SW_TOKENS, N - n0);
   const half_t* lg = logits + (static_cast<int64_t>(b) * N + n0) * GM;
+  const int nh = ntok * GM;
+  if (vec) {
+    for (int i = threadIdx.x; i < nh / 8; i += 256)
+      reinterpret_cast<int4_t*>(lh)[i] = reinterpret_cast<const int4_t*>(lg)[i];
+  } else {
+    for (int i = threadIdx.x; i < nh; i += 256) lh[i] = lg[i];
+  }
   const float* cb = c + b * c_stride;
   float bi[M];
 #pragma unroll
-  for (int m = 0; m < M; ++m) bi[m] = bias[m];
-  for (int p = threadIdx.x; p < SW_TOKENS * G; p += 256) {
-    const int t = p / G, h = p % G;
-    float l[M];
-    float mx = -INFINITY;
+  for (int m = 0; m < M; ++m) bi[m] = -bias[m] * LOG2E;
+  __syncthreads();
+  float w[PMAX][M];
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      l[m] = t < ntok ? static_cast<float>(lg[static_cast<int64_t>(t) * GM + h * M + m]) + cb[h * M + m] : 0.f;
-      mx = fmaxf(mx, l[m]);
+  for (int k = 0; k < PMAX; ++k) {
+    const int p = threadIdx.x + 256 * k, t = p / G, h = p % G;
+    if (t < ntok) {
+      float l[M];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        l[m] = static_cast<float>(lh[p * M + m]) + cb[h * M + m];
+        mx = fmaxf(mx, l[m]);
+      }
+      float s = 0.f;
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        w[k][m] = __builtin_amdgcn_exp2f((l[m] - mx) * LOG2E);
+        s += w[k][m];
+      }
+      const float inv = __builtin_amdgcn_rcpf(s);
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+        w[k][m] = w[k][m] * inv * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(__builtin_fmaf(-l[m], LOG2E, bi[m])));
     }
-    float e[M], s = 0.f;
+  }
+  __syncthreads();  // every logit is read: the tile may overwrite them
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      e[m] = __expf(l[m] - mx);
-      s += e[m];
-    }
-    const float inv = 1.f / s;
+  for (int k = 0; k < PMAX; ++k) {
+    const int p = threadIdx.x + 256 * k, t = p / G, h = p % G;
+    if (t < SW_TOKENS) {
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      const float gate = 1.f / (1.f + __expf(-(l[m] + bi[m])));
-      tile[(h * M + m) * (SW_TOKENS + 1) + t] = t < ntok ? e[m] * inv * gate : 0.f;
+      for (int m = 0; m < M; ++m) tile[(h * M + m) * (SW_TOKENS + 1) + t] = t < ntok ? w[k][m] : 0.f;
     }
   }
   __syncthreads();
-  // rows of the transposed tile: each half-wave takes one query column at a time, a lane per token
+  // each column's sum over the block's 32 tokens (zeros past ntok), one thread per column, in token order
+  for (int j = threadIdx.x; j < GM; j += 256) {
+    float s = 0.f;
+#pragma unroll 8
+    for (int t = 0; t < SW_TOKENS; ++t) s += tile[j * (SW_TOKENS + 1) + t];
+    partial[(static_cast<int64_t>(b) * gridDim.x + blockIdx.x) * GM + j] = s;
+  }
+  // rows of the transposed tile: each half-wave takes every eighth query column, a lane per token
   const int half = threadIdx.x >> 5, lane = threadIdx.x & 31;
-  for (int j = half; j < GM; j += 8) {
-    const float w = tile[j * (SW_TOKENS + 1) + lane];
-    if (lane < ntok) a_t[(static_cast<int64_t>(b) * GM + j) * N + n0 + lane] = static_cast<half_t>(w);
-    float s = w;
-#pragma unroll
-    for (int m = 16; m; m >>= 1) s += xor_shuffle(s, m);
-    if (lane == 0) partial[(static_cast<int64_t>(b) * gridDim.x + blockIdx.x) * GM + j] = s;
+  if (lane < ntok) {
+    half_t* orow = a_t + static_cast<int64_t>(b) * GM * N + n0 + lane;
+#pragma unroll 4
+    for (int j = half; j < GM; j += 8)
+      orow[static_cast<int64_t>(j) * N] = static_cast<half_t>(tile[j * (SW_TOKENS + 1) + lane]);
   }
 }
 
@@ -241,14 +272,16 @@ extern "C" int ff_slot_weights(const void* logits, const float* c, int64_t c_str
   if (!logits || !c || !bias || !a_t || !partial) return fail(FF_EINVAL, "slot_weights: null pointer");
   const size_t smem = static_cast<size_t>(G * M) * (SW_TOKENS + 1) * sizeof(float);
   if (smem > 64 * 1024) return fail(FF_EINVAL, "slot_weights: G*M too large (LDS tile above 64 KB)");
+  // the fp16 logits block (64 G M bytes) fits in the tile's LDS, and 32 G pairs fit the kernel's 256 PMAX
+  const int vec = (G * M) % 8 == 0 && reinterpret_cast<uintptr_t>(logits) % 16 == 0;
   const dim3 grid(static_cast<unsigned>(ff_slot_weights_blocks(N)), static_cast<unsigned>(B));
   const hipStream_t st = as_stream(stream);
   const auto* pl = static_cast<const half_t*>(logits);
   auto* pa = static_cast<half_t*>(a_t);
   const int Ni = static_cast<int>(N), Gi = static_cast<int>(G);
   if (M == 6)
-    slot_weights_kernel<6><<<grid, 256, smem, st>>>(pl, c, c_stride, bias, Ni, Gi, pa, partial);
+    slot_weights_kernel<6><<<grid, 256, smem, st>>>(pl, c, c_stride, bias, Ni, Gi, vec, pa, partial);
   else
-    slot_weights_kernel<18><<<grid, 256, smem, st>>>(pl, c, c_stride, bias, Ni, Gi, pa, partial);
+    slot_weights_kernel<18><<<grid, 256, smem, st>>>(pl, c, c_stride, bias, Ni, Gi, vec, pa, partial);
   return check_launch("slot_weights");
 }
