@@ -121,9 +121,14 @@ constexpr int stage_bytes() {
 // row-contiguous instead of 16 bytes per row. QKV stages y itself and rotates in the row layout, where the 8 lanes
 // of a row read that row's RoPE table entries as 16-byte runs instead of 32 scattered rows per load. `stage` is this
 // wave's private area of stage_bytes<EPI, NI>().
+// Tile metadata staged in LDS (the persistent kernel): the tile's 256 column scales, 256 biases and 256 row scales,
+// in that order, 1 KB each.
+constexpr int META_BYTES = 3 * 1024;
+
 template <int EPI, int NI, int MI>
 __device__ __forceinline__ void store_epilogue(const int16_t_v (&acc)[NI][MI], int m_base, int n_base, int lane,
-                                               const GemmArgs& args, uint8_t* stage) {
+                                               const GemmArgs& args, uint8_t* stage, const uint8_t* meta = nullptr,
+                                               int row0 = 0, int col0 = 0) {
   const int M = args.M, N = args.N;
   const int fr = lane & 31, fk = lane >> 5;
   if constexpr (EPI == FF_EPI_I32) {  // debug output: raw accumulators, stored from registers
@@ -165,9 +170,14 @@ __device__ __forceinline__ void store_epilogue(const int16_t_v (&acc)[NI][MI], i
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const uint32_t off = static_cast<uint32_t>(32 * i + 8 * q + 4 * fk) * 4;
-        const int nb = buf_bytes(static_cast<int64_t>(N - n_base) * 4);
-        cs[i][q] = buf_load_f4(args.col_scale + n_base, nb, off);
-        bi[i][q] = buf_load_f4(args.bias + n_base, nb, off);
+        if (meta) {
+          cs[i][q] = *reinterpret_cast<const float4_t*>(meta + col0 * 4 + off);
+          bi[i][q] = *reinterpret_cast<const float4_t*>(meta + 1024 + col0 * 4 + off);
+        } else {
+          const int nb = buf_bytes(static_cast<int64_t>(N - n_base) * 4);
+          cs[i][q] = buf_load_f4(args.col_scale + n_base, nb, off);
+          bi[i][q] = buf_load_f4(args.bias + n_base, nb, off);
+        }
       }
     // Per-row inputs are software-pipelined: the row scale of block j + 1 is loaded as soon as block j's results are
     // computed, and the residual rows (or RoPE table rows) of block j + 1 as soon as block j is stored, so their
@@ -189,8 +199,11 @@ __device__ __forceinline__ void store_epilogue(const int16_t_v (&acc)[NI][MI], i
     };
     auto load_row = [&](int j) __attribute__((always_inline)) {
       // rows past M read 0 (computed, never stored)
-      rs = buf_load_f1(args.row_scale + m_base, buf_bytes(static_cast<int64_t>(M - m_base) * 4),
-                       static_cast<uint32_t>(32 * j + fr) * 4);
+      if (meta)
+        rs = *reinterpret_cast<const float*>(meta + 2048 + (row0 + 32 * j + fr) * 4);
+      else
+        rs = buf_load_f1(args.row_scale + m_base, buf_bytes(static_cast<int64_t>(M - m_base) * 4),
+                         static_cast<uint32_t>(32 * j + fr) * 4);
     };
     // QKV: RoPE table row (m mod rope_len) of the lane's pass row, kept incrementally: the rows of block j, pass p
     // are rope_row0 + 32 j + p ROWS_PER_PASS (at most 32 MI - 1 past it), wrapped by at most one subtraction when
@@ -745,9 +758,15 @@ __device__ __forceinline__ void tail_block(const GemmArgs& args, int m_first, in
 // workgroup per CU, each takes every G-th tile of the grouped order, and slices are one stream, so the next tile's
 // first slice loads under the current tile's last MFMAs and its first fragments are read before the epilogue. No
 // workgroup starts cold, and row tiles that reach past M are ordered last (their rows past M load as zeros, and
-// MFMAs on zeros draw less power, so the partial last round runs at a higher clock). The epilogue stages through
+// MFMAs on zeros draw less power, so the partial last round runs at a higher clock). A tile's column scales, biases
+// and row scales load into LDS with its first slice (buffer->LDS, three waves, 1 KB each), so the epilogue reads
+// them from LDS instead of waiting ~2000 cycles for global loads issued at its start. The epilogue stages through
 // the ring slot of the tile's last slice, which no load targets until the barrier after the epilogue; when eight
-// staging areas do not fit in one slot (QKV), the last ones use a spare area past the ring.
+// staging areas do not fit in one slot (QKV), the last ones use a spare area past the ring. SwiGLU's small staging
+// areas (18 KB for eight waves) sit past the ring instead, so its waves skip that barrier: a wave that finishes its
+// epilogue early starts the next tile's products while slower waves finish theirs, and the next slice barrier
+// joins them (measured per wave with s_memtime at fc1's batch-32 shape: the barrier had cost ~2000 cycles per tile
+// of waiting for the slowest wave).
 
 template <int EPI>
 __global__ __launch_bounds__(512, 1) void gemm_s8_persist_kernel(const GemmArgs args, int m_full) {
@@ -758,8 +777,17 @@ __global__ __launch_bounds__(512, 1) void gemm_s8_persist_kernel(const GemmArgs 
   constexpr int CPR = RK / 16;               // 16-byte chunks per row
   constexpr int KSTEPS = RK / 32;            // 32-byte MFMA k-steps per slot (even: a slot starts in buffer 0)
   constexpr int SB = stage_bytes<EPI, NI>();
-  constexpr int FIT = STAGE / SB < 8 ? STAGE / SB : 8;  // staging areas inside the free slot
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE + (8 - FIT) * SB];
+  // The tile metadata (column scales, biases, row scales) loads into LDS with the tile's first slice, into one of
+  // two buffers by tile parity. SwiGLU's staging areas fit beside the ring, so its waves need not wait for each other
+  // after the epilogue; the other epilogues stage through the free ring slot (the last slots past the ring when
+  // eight areas do not fit in it).
+  constexpr bool META = EPI != FF_EPI_I32;
+  constexpr bool OWN_STAGE = EPI == FF_EPI_SWIGLU;
+  constexpr int FIT = OWN_STAGE ? 0 : (STAGE / SB < 8 ? STAGE / SB : 8);
+  constexpr int META_OFF = 2 * STAGE;
+  constexpr int STAGE_OFF = META_OFF + 2 * META_BYTES;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGE_OFF + (8 - FIT) * SB];
+  static_assert(STAGE_OFF + (8 - FIT) * SB <= 160 * 1024, "LDS");
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -809,6 +837,19 @@ __global__ __launch_bounds__(512, 1) void gemm_s8_persist_kernel(const GemmArgs 
         buffer_to_lds(abase, an, st + blk * 1024, voff);
       else
         buffer_to_lds(wbase, wn_, st + blk * 1024, voff);
+    }
+    if constexpr (META) {
+      if (ikt == 0 && wave < 3) {  // the tile's metadata, 1 KB per wave: column scales, biases, row scales
+        uint8_t* md = smem + META_OFF + (ir & 1) * META_BYTES + wave * 1024;
+        const int nb = nrec(static_cast<int64_t>(N - in0) * 4);
+        if (wave == 0)
+          buffer_to_lds(args.col_scale + in0, nb, md, static_cast<uint32_t>(lane) * 16);
+        else if (wave == 1)
+          buffer_to_lds(args.bias + in0, nb, md, static_cast<uint32_t>(lane) * 16);
+        else
+          buffer_to_lds(args.row_scale + im0, nrec(static_cast<int64_t>(M - im0) * 4), md,
+                        static_cast<uint32_t>(lane) * 16);
+      }
     }
     ++ig;
     if (++ikt == KT) {
@@ -900,14 +941,20 @@ __global__ __launch_bounds__(512, 1) void gemm_s8_persist_kernel(const GemmArgs 
     }
     // Every wave has read all of the tile's last slice g - 1 (barrier above): its slot is the staging area until
     // the barrier below, after which slice g + 1 may load into it.
-    uint8_t* stage = wave < FIT ? smem + ((g - 1) & 1) * STAGE + wave * SB : smem + 2 * STAGE + (wave - FIT) * SB;
+    uint8_t* stage = wave < FIT ? smem + ((g - 1) & 1) * STAGE + wave * SB : smem + STAGE_OFF + (wave - FIT) * SB;
     // An opaque lane index keeps the epilogue's lane-derived offsets from being hoisted out of the tile loop,
     // where they would hold registers through the main loop.
     int el = lane;
     asm volatile("" : "+v"(el));
-    store_epilogue<EPI, NI, MI>(acc, m0 + wm * WM, n0 + wn * WN, el, args, stage);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
+    const uint8_t* md = META ? smem + META_OFF + (r & 1) * META_BYTES : nullptr;
+    store_epilogue<EPI, NI, MI>(acc, m0 + wm * WM, n0 + wn * WN, el, args, stage, md, wm * WM, wn * WN);
+    // Staging in the ring slot: every wave must be done with it before the next slice loads into it. With their own
+    // staging areas the waves go on (the next tile's first slice barrier joins them), except for one-slice tiles,
+    // whose next metadata load could overwrite the buffer a slower wave still reads.
+    if (!OWN_STAGE || KT < 2) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+    }
     // The next slice's first fragments again: the copies read above are dead on this path, so they do not stay
     // live through the epilogue.
     read_frags(g, 0, 0);

@@ -1,7 +1,10 @@
 """The EVA02 tagger's float forward and the single W8A8 linear in PyTorch on the CPU: the CPU baseline.
 
 Test and measurement infrastructure, like the rest of this package: `bench.py`'s `cpu_baseline` leg times these on
-the host cores, and the tests check them against the numpy restatements. Nothing in the product imports them.
+the host cores. tests/test_oracle.py pins them against the numpy restatements: `forward_float`'s logits against
+`model.head_logits(model.forward_float_x(...))` (float64) on a 2-block model, `rot_q8` code for code and scale for
+scale against `rotq8.rot_q8_1024`, and `w8a8_linear` within one fp16 ulp of `rotq8.rot_q8_1024` followed by
+`gemm.gemm_s8(..., EPI_BIAS_F16)`. Nothing in the product imports them.
 
 `forward_float` follows the op order of the reference's PyTorch model (foidfinder/backends/cuda/reference.py:109-131:
 patch GEMM + positions, per block LayerNorm -> qkv linear -> RoPE on q and k -> scaled-dot-product attention -> proj
@@ -10,9 +13,11 @@ axial RoPE on the patch tokens only (foidfinder/backends/mlx/haruka.py:22-33), a
 (foidfinder/backends/mlx/haruka.py:86-99), in fp32 throughout.
 
 `w8a8_linear` is the plumbing config's single linear on the CPU: the 1024-point Walsh-Hadamard rotation of the
-activations, per-token symmetric int8 quantization (foidfinder/backends/cuda/csrc/kernels.cu:49-108), the int8 x int8
-product accumulated exactly (fp32 products of integers below 2^24 in magnitude are exact, K * 127^2 < 2^24 for
-K <= 1040), and the dequant + bias epilogue (gemm.cuh:135-136).
+activations in the reference's butterfly order, per-token symmetric int8 quantization (`rot_q8`,
+foidfinder/backends/cuda/csrc/kernels.cu:13-108), the int8 x int8 product accumulated exactly (fp32 products of
+integers below 2^24 in magnitude are exact, K * 127^2 < 2^24 for K <= 1040), and the dequant + bias epilogue
+(gemm.cuh:135-136; here `acc * rs * cs + bias` rounds after each operation, where the reference's compiler fuses the
+last multiply and add).
 """
 
 from __future__ import annotations
@@ -57,21 +62,28 @@ def forward_float(images: torch.Tensor, raw: dict[str, torch.Tensor], depth: int
 
 
 def fwht_1024(x: torch.Tensor) -> torch.Tensor:
-    """Rows of x [M, 1024] times the normalized Sylvester Hadamard matrix, in fp32 butterflies."""
+    """Rows of x [M, 1024] times the normalized Sylvester Hadamard matrix, in fp32 butterflies over the column bits
+    in the reference's stage order 0, 1, 2, 8, 9, 3, 4, 5, 6, 7 (kernels.cu:13-47), then x 1/32."""
     m = x.shape[0]
-    half = 1
-    while half < 1024:
-        v = x.view(m, 1024 // (2 * half), 2, half)
+    for bit in (0, 1, 2, 8, 9, 3, 4, 5, 6, 7):
+        half = 1 << bit
+        v = x.reshape(m, 1024 // (2 * half), 2, half)
         x = torch.stack((v[:, :, 0] + v[:, :, 1], v[:, :, 0] - v[:, :, 1]), dim=2).reshape(m, 1024)
-        half *= 2
     return x * 0.03125
+
+
+@torch.no_grad()
+def rot_q8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """x fp16 [M, 1024] -> (int8 codes as fp32 [M, 1024], fp32 row scale [M]): rotate, then per-token absmax int8
+    (scale = max(amax, 1e-12) / 127, codes = clamp(round-half-even(v * (1 / scale)), -127, 127); kernels.cu:93-107)."""
+    v = fwht_1024(x.float())
+    scale = v.abs().amax(1).clamp_min(1e-12) / 127.0
+    return torch.round(v * (1.0 / scale)[:, None]).clamp_(-127, 127), scale
 
 
 @torch.no_grad()
 def w8a8_linear(x: torch.Tensor, qweight: torch.Tensor, wscale: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
     """x fp16 [M, 1024] -> fp16 [M, N]: rotate, quantize per token, exact int8 product, dequantize, add bias."""
-    v = fwht_1024(x.float())
-    scale = v.abs().amax(1).clamp_min(1e-12) / 127.0
-    codes = torch.round(v * (1.0 / scale)[:, None]).clamp_(-127, 127)
+    codes, scale = rot_q8(x)
     acc = codes @ qweight.float().t()  # integer-valued fp32, exact for K * 127^2 < 2^24
     return (acc * scale[:, None] * wscale[None, :] + bias[None, :]).half()

@@ -11,9 +11,10 @@ forward differs from the unquantized float forward by the same amount). Hence:
   2. attention per block: within 4e-3 absolute of float64 attention on the engine's own qkv;
   3. end to end on a small model (2 blocks, 112 px): |p_engine - p_oracle_int8| within 1.5x the int8 noise budget
      |p_oracle_int8 - p_float| (max and mean over tags and images), with the logits finite;
-  4. end to end at the benchmark's model (24 blocks, 1025 tokens) against stated absolute bars (E2E_BARS and
-     E2E_RMS_REL_X): max and mean |dp|, max |dlogit|, the reference's decision-stability rule, the same top-1 tag and
-     gap-filtered top-k, against both the int8 oracle and the float forward.
+  4. end to end at the benchmark's model (24 blocks, 1025 tokens) against stated bars (E2E_REL_MAX, E2E_MEAN_DP and
+     E2E_RMS_REL_X): max |dp| and max |dlogit| within a stated multiple of the int8 noise measured on the same images
+     (the int8 oracle against the float forward), mean |dp|, the reference's decision-stability rule, the same top-1
+     tag and gap-filtered top-k, against both the int8 oracle and the float forward.
 """
 
 from __future__ import annotations
@@ -172,11 +173,14 @@ def test_full_size_batch_32_is_permutation_equivariant(dev):
     assert torch.equal(shuffled, full[perm]), "permuting the batch does not permute the logits"
 
 
-# The stated end-to-end bar at the benchmark's model (EVA02-L/14-448, 24 blocks, 1025 tokens), without teacher
-# forcing, against each reference: (max |dp|, mean |dp|, max |dlogit|) over all tags of both images. Reasoning and
-# measurements are in the docstring of the test.
-E2E_BARS = {"int8 oracle": (0.15, 0.005, 0.8), "float": (0.15, 0.005, 1.0)}
+# The stated end-to-end bars at the benchmark's model (EVA02-L/14-448, 24 blocks, 1025 tokens), without teacher
+# forcing, against each reference: max |dp| and max |dlogit| over all tags and images at most E2E_REL_MAX times the
+# int8 noise (the same maxima of the int8 oracle against the float forward, on the same images), mean |dp| at most
+# E2E_MEAN_DP. Reasoning and measurements are in the docstring of the test.
+E2E_REL_MAX = {"int8 oracle": 1.1, "float": 1.25}
+E2E_MEAN_DP = 0.005
 E2E_RMS_REL_X = 0.12  # rms(x_engine - x_oracle) / rms(x_oracle) for the residual stream after the last block
+E2E_IMAGES = 6  # seeded images through the full-depth end-to-end comparison
 
 
 def decision_flips(p, p_ref):
@@ -204,7 +208,7 @@ def gap_filtered_topk(logits, ref, kmax=50):
 
 @pytest.mark.timeout(900)
 def test_full_depth_eva02_l_end_to_end(dev):
-    """EVA02-L/14-448 (24 blocks, 1025 tokens) on 2 seeded images through the served path (graph replay), against the
+    """EVA02-L/14-448 (24 blocks, 1025 tokens) on E2E_IMAGES seeded images through the served path (graph replay), against the
     int8 oracle forward and against the float64 forward of the same weights, with no teacher forcing.
 
     Why these bars. Every block kernel is bit-exact with the oracle on identical inputs except attention (fp32 MFMA
@@ -213,15 +217,18 @@ def test_full_depth_eva02_l_end_to_end(dev):
     percent of the codes by one step; such flips recur in every block, and the engine and the int8 oracle drift apart
     like two int8 models with independent rounding. Measured at this seed: rms relative difference of the residual
     stream 1.2 % after block 1 and 8.2 % after block 24, against 2.0 % and 10.0 % between the int8 oracle and the
-    float forward (the int8 noise itself); logits differ by up to ~0.6 (engine vs int8 oracle) and ~0.75 (vs float),
-    with head weights N(0, 0.05) over LayerNorm outputs (logit spread 1.6). Sigmoid outputs therefore cannot agree to
-    2e-3. The bars: the reference's own for its int8 engine against the fp32 model, max |dp| < 0.15
-    (tests/test_cuda_engine.py:54), against both references (measured 0.122 and 0.133); mean |dp| <= 0.005
-    (measured 0.0022 and 0.0026; the reference's 1e-4 is for its real checkpoint, where nearly every tag sits at
-    p ~ 0) and max |dlogit| as in E2E_BARS; the reference's decision-stability rule
-    (tests/test_cuda_engine.py:55-57) with no violation; the same top-1 tag; and identical
-    top-k for every k <= 50 where the reference's logit gap between ranks k and k + 1 exceeds twice the image's
-    largest logit error (checked for at least one k). The head's bias is spread like a trained tagger's output:
+    float forward (the int8 noise itself). On the 6 images the int8 oracle itself differs from the float forward by
+    max |dp| 0.158 (per image 0.116, 0.148, 0.139, 0.109, 0.158, 0.128) and max |dlogit| 0.995, with head weights
+    N(0, 0.05) over LayerNorm outputs: sigmoid outputs cannot agree to 2e-3, and the reference's own bar for its int8
+    engine against the fp32 model on its real checkpoint, max |dp| < 0.15 (tests/test_cuda_engine.py:54), is below
+    this synthetic model's int8 noise. The engine measured max |dp| 0.138 and max |dlogit| 0.759 against the int8
+    oracle (0.87 and 0.76 of the noise), 0.147 and 0.984 against the float forward (0.93 and 0.99). The bars: max
+    |dp| and max |dlogit| at most 1.1 times the noise against the int8 oracle and 1.25 times against the float
+    forward (E2E_REL_MAX: the engine is one more int8 model whose maxima over a few images scatter like the
+    oracle's); mean |dp| <= 0.005 (measured 0.0024 and 0.0028; the reference's 1e-4 is for its real checkpoint,
+    where nearly every tag sits at p ~ 0); the reference's decision-stability rule (tests/test_cuda_engine.py:55-57)
+    with no violation; the same top-1 tag; and identical top-k for every k <= 50 where the reference's logit gap
+    between ranks k and k + 1 exceeds twice the image's largest logit error (checked for at least one k). The head's bias is spread like a trained tagger's output:
     N(-6, 2^2) for most tags (confidently absent, with a tail near 0.5 for the decision rule) and 12 confident tags
     2.5 logits apart, so that ties do not decide the top-k."""
     from foidfinder_amd.engine import Eva02Config, Eva02Int8, convert_checkpoint, synthetic_checkpoint
@@ -235,8 +242,8 @@ def test_full_depth_eva02_l_end_to_end(dev):
     raw["head.bias"] = bias
     state = convert_checkpoint(raw, cfg)
     eng = Eva02Int8(state, cfg, device=dev)
-    images = OM.synthetic_images(2, cfg.img_size, seed=8)
-    print("full-depth end to end: engine forward (graph, batch 2)", flush=True)
+    images = OM.synthetic_images(E2E_IMAGES, cfg.img_size, seed=8)
+    print(f"full-depth end to end: engine forward (graph, batch {E2E_IMAGES})", flush=True)
     served = eng(torch.from_numpy(images).to(dev)).cpu().numpy().astype(np.float64)
     trace = {}
     eager = eng.eager(torch.from_numpy(images).to(dev), trace).cpu().numpy().astype(np.float64)
@@ -253,12 +260,15 @@ def test_full_depth_eva02_l_end_to_end(dev):
     def job(arg):
         kind, i = arg
         one = images[i : i + 1]
-        return OM.forward_int8_x(one, fw, qblocks) if kind == "int8" else OM.forward_float_x(one, fweights)
+        out = OM.forward_int8_x(one, fw, qblocks) if kind == "int8" else OM.forward_float_x(one, fweights)
+        print(f"full-depth end to end: oracle {kind} forward of image {i} done", flush=True)
+        return out
 
     print("full-depth end to end: oracle int8 and float64 forwards", flush=True)
+    n = E2E_IMAGES
     with ThreadPoolExecutor(4) as ex:
-        xs = list(ex.map(job, [("int8", 0), ("int8", 1), ("float", 0), ("float", 1)]))
-    x_int8, x_float = np.concatenate(xs[:2]), np.concatenate(xs[2:])
+        xs = list(ex.map(job, [("int8", i) for i in range(n)] + [("float", i) for i in range(n)]))
+    x_int8, x_float = np.concatenate(xs[:n]), np.concatenate(xs[n:])
     ref_int8, ref_float = OM.head_logits(x_int8, fw), OM.head_logits(x_float, fweights)
 
     rms = lambda d, r: float(np.sqrt((d.astype(np.float64) ** 2).mean() / (r.astype(np.float64) ** 2).mean()))
@@ -267,22 +277,26 @@ def test_full_depth_eva02_l_end_to_end(dev):
     sig = lambda z: 1.0 / (1.0 + np.exp(-z))
     p = sig(served)
     report = [f"residual stream after block 24: engine vs int8 oracle rms rel {drift:.4f}, "
-              f"int8 oracle vs float {noise:.4f}"]
+              f"int8 oracle vs float {noise:.4f}; int8 noise (int8 oracle vs float): max|dp| "
+              f"{np.abs(sig(ref_int8) - sig(ref_float)).max():.4f} max|dlogit| {np.abs(ref_int8 - ref_float).max():.4f}"]
     for name, ref in (("int8 oracle", ref_int8), ("float", ref_float)):
         dp, dl = np.abs(p - sig(ref)), np.abs(served - ref)
         checked, bad = gap_filtered_topk(served, ref)
         report.append(f"vs {name}: max|dp| {dp.max():.4f} mean {dp.mean():.5f}; max|dlogit| {dl.max():.4f} "
-                      f"mean {dl.mean():.4f}; decision flips {decision_flips(p, sig(ref))}; top-1 "
-                      f"{[int(np.argmax(served[i]) == np.argmax(ref[i])) for i in range(2)]}; gap-filtered top-k "
+                      f"mean {dl.mean():.4f}; per image max|dp| {np.round(dp.max(1), 4).tolist()} max|dlogit| "
+                      f"{np.round(dl.max(1), 3).tolist()}; decision flips {decision_flips(p, sig(ref))}; top-1 "
+                      f"{[int(np.argmax(served[i]) == np.argmax(ref[i])) for i in range(n)]}; gap-filtered top-k "
                       f"checked {checked}, mismatched {bad}")
     print("\n".join(report), flush=True)
     assert drift <= E2E_RMS_REL_X, report[0]
+    noise_dp = np.abs(sig(ref_int8) - sig(ref_float)).max()
+    noise_dl = np.abs(ref_int8 - ref_float).max()
     for name, ref in (("int8 oracle", ref_int8), ("float", ref_float)):
-        max_dp, mean_dp, max_dl = E2E_BARS[name]
+        rel = E2E_REL_MAX[name]
         dp, dl = np.abs(p - sig(ref)), np.abs(served - ref)
-        assert dp.max() <= max_dp and dp.mean() <= mean_dp, report
-        assert dl.max() <= max_dl, report
+        assert dp.max() <= rel * noise_dp and dp.mean() <= E2E_MEAN_DP, report
+        assert dl.max() <= rel * noise_dl, report
         assert decision_flips(p, sig(ref)) == 0, report
-        assert all(np.argmax(served[i]) == np.argmax(ref[i]) for i in range(2)), report
+        assert all(np.argmax(served[i]) == np.argmax(ref[i]) for i in range(n)), report
         checked, bad = gap_filtered_topk(served, ref)
         assert checked > 0 and not bad, report

@@ -194,6 +194,29 @@ def test_gemm_s8_epilogue_bit_exact(dev, rng, epi, variant):
 
 
 @pytest.mark.parametrize("variant", GEMM_VARIANTS)
+def test_w8a8_linear_chain_bit_exact(dev, variant):
+    """The plumbing config's single W8A8 linear at full size, with its own generator (fp16 [1025, 1024] ~ N(0, 1) with
+    1 % of channels x20, weights N(0, 0.02) rotated and quantized per row with fp16-rounded scales, bias N(0, 0.02)):
+    rot_q8_1024 then gemm_s8 with the bias epilogue at N = 3072, as the reference chains the two ops
+    (kernels.cu:187-235). Codes, fp32 row scales and fp16 outputs bit-exact with the oracle's chain."""
+    from foidfinder_amd import kernels as K
+
+    x, qw, ws, b = OM.w8a8_linear_inputs()
+    a8 = torch.empty(x.shape, dtype=torch.int8, device=dev)
+    rs = torch.empty(x.shape[0], dtype=torch.float32, device=dev)
+    K.rot_q8_1024(to_gpu(x, dev), None, None, a8, rs)
+    y = torch.empty(x.shape[0], qw.shape[0], dtype=torch.float16, device=dev)
+    K.gemm_s8(a8, to_gpu(qw, dev), rs, to_gpu(ws, dev), to_gpu(b, dev), y, K.EPI_BIAS_F16, variant, None, None, 1.0)
+    torch.cuda.synchronize()
+    q0, s0 = OR.rot_q8_1024(x)
+    assert_codes_equal((a8.cpu().numpy(), rs.cpu().numpy()), (q0, s0), "config-1 rotation")
+    want = OG.gemm_s8(q0, qw, s0, ws, b, OG.EPI_BIAS_F16)
+    got = y.cpu().numpy()
+    bad = np.argwhere(got.view(np.uint16) != want.view(np.uint16))
+    assert bad.size == 0, f"{len(bad)} outputs differ, first at {bad[:4].tolist()}"
+
+
+@pytest.mark.parametrize("variant", GEMM_VARIANTS)
 @pytest.mark.parametrize("rope_len", [1, 5, 8, 65, 200])
 def test_gemm_s8_qkv_short_rope_tables(dev, rng, rope_len, variant):
     # RoPE table row m % rope_len for tables shorter than a wave's rows (several wraps inside one output block), of a
@@ -405,20 +428,28 @@ def test_layer_norm2_matches_two_float_layer_norms(dev, rng):
         assert np.abs(out.cpu().numpy().astype(np.float64) - want).max() < 8e-3 * max(1.0, np.abs(want).max())
 
 
-@pytest.mark.parametrize(("B", "N", "G", "M", "shared_c"), [(2, 1025, 16, 6, True), (3, 65, 16, 18, False),
-                                                             (1, 31, 4, 18, False), (2, 96, 16, 18, True)])
-def test_slot_weights_matches_float(dev, rng, B, N, G, M, shared_c):
+@pytest.mark.parametrize(("B", "N", "G", "M", "shared_c", "offset"),
+                         [(2, 1025, 16, 6, True, 0), (3, 65, 16, 18, False, 0), (1, 31, 4, 18, False, 0),
+                          (2, 96, 16, 18, True, 0),
+                          # the pair loops' bounds (G = 64 at M = 6 and G = 27 at M = 18 fill the kernel's pairs per
+                          # thread), G*M not a multiple of 8 (2-byte logit copies), and a logits view one fp16 element
+                          # past a 16-byte boundary (2-byte copies although G*M % 8 == 0)
+                          (1, 40, 64, 6, True, 0), (2, 33, 27, 18, False, 0), (1, 50, 3, 6, True, 0),
+                          (2, 70, 16, 6, False, 1)])
+def test_slot_weights_matches_float(dev, rng, B, N, G, M, shared_c, offset):
     """ff_slot_weights: softmax over the M queries times sigmoid(logit + bias), transposed, and the per-block sums
     over the tokens (summed over blocks: each query's mass), against float64."""
     from foidfinder_amd import kernels as K
 
     logits = (rng.standard_normal((B, N, G * M)) * 3).astype(np.float16)
+    lg = torch.empty(B * N * G * M + offset, dtype=torch.float16, device=dev)[offset:].view(B, N, G * M)
+    lg.copy_(to_gpu(logits, dev))
     c = (rng.standard_normal(G * M if shared_c else (B, G * M)) * 0.5).astype(np.float32)
     bias = (-2 + 0.3 * rng.standard_normal(M)).astype(np.float32)
     nblk = K.slot_weights_blocks(N)
     a_t = torch.full((B, G * M, N), 7.0, dtype=torch.float16, device=dev)
     partial = torch.empty(B, nblk, G * M, dtype=torch.float32, device=dev)
-    K.slot_weights(to_gpu(logits, dev), to_gpu(c, dev), to_gpu(bias, dev), G, a_t, partial)
+    K.slot_weights(lg, to_gpu(c, dev), to_gpu(bias, dev), G, a_t, partial)
     torch.cuda.synchronize()
     l = logits.astype(np.float64).reshape(B, N, G, M) + c.astype(np.float64).reshape(-1, 1, G, M)
     e = np.exp(l - l.max(-1, keepdims=True))

@@ -417,6 +417,81 @@ def test_int8_forward_tracks_float_forward():
     assert np.abs(p8 - pf).max() < 0.05 and np.abs(p8 - pf).mean() < 0.01
 
 
+# ---------------- the CPU baseline's PyTorch restatement (oracle/float_torch.py) ----------------
+
+
+def _float_torch_pair(seed=3):
+    """A 2-block EVA02 at 56 px: the engine's float state dict (for float_torch) and the same weights as the numpy
+    oracle's FloatWeights."""
+    torch = pytest.importorskip("torch")
+    from foidfinder_amd.engine import Eva02Config, eva02_rope_tables, synthetic_checkpoint
+    from oracle import float_torch as FT
+
+    cfg = Eva02Config(img_size=56, depth=2, tags=64)
+    raw = synthetic_checkpoint(cfg, seed=seed)
+    n = {k: v.numpy() for k, v in raw.items()}
+    w = OM.FloatWeights(cfg=OM.Eva02Config(img_size=56, depth=2, tags=64), patch_w=n["patch_embed.weight"],
+                        patch_b=n["patch_embed.bias"], cls=n["cls_token"], pos=n["pos_embed"], norm_w=n["norm.weight"],
+                        norm_b=n["norm.bias"], head_w=n["head.weight"], head_b=n["head.bias"])
+    names = {"norm1_w": "norm1.weight", "norm1_b": "norm1.bias", "qkv_w": "attn.qkv.weight", "qkv_b": "attn.qkv.bias",
+             "proj_w": "attn.proj.weight", "proj_b": "attn.proj.bias", "norm2_w": "norm2.weight",
+             "norm2_b": "norm2.bias", "fc1_w": "mlp.fc1.weight", "fc1_b": "mlp.fc1.bias",
+             "mlp_norm_w": "mlp.norm.weight", "mlp_norm_b": "mlp.norm.bias", "fc2_w": "mlp.fc2.weight",
+             "fc2_b": "mlp.fc2.bias"}
+    for i in range(cfg.depth):
+        w.blocks.append({k: n[f"blocks.{i}.{v}"] for k, v in names.items()})
+    images = OM.synthetic_images(2, 56, seed=5)
+    run = lambda: FT.forward_float(torch.from_numpy(images).float(), raw, cfg.depth, cfg.heads, cfg.patch,  # noqa
+                                   cfg.hidden, eva02_rope_tables(cfg.grid, cfg.rope_ref), cfg.eps).numpy()
+    return run, OM.head_logits(OM.forward_float_x(images, w), w)
+
+
+def test_float_torch_forward_matches_float64_forward():
+    """bench.py's CPU baseline workload: the fp32 PyTorch forward against the numpy float64 forward of the same
+    weights (measured max |dlogit| 1.9e-3 at logits up to 3.4: fp32 rounding through two blocks)."""
+    run, want = _float_torch_pair()
+    got = run()
+    assert np.abs(got - want).max() < 5e-3
+
+
+def test_float_torch_check_catches_a_dropped_rope(monkeypatch):
+    pytest.importorskip("torch")
+    from oracle import float_torch as FT
+
+    run, want = _float_torch_pair()
+    monkeypatch.setattr(FT, "_rope", lambda x, cos, sin: x)
+    assert np.abs(run() - want).max() > 5e-3
+
+
+def test_float_torch_rot_q8_equals_the_oracle(rng):
+    """The CPU baseline's rotation + quantization takes the reference's butterfly order and division sequence, so it
+    reproduces the oracle's codes and fp32 scales bit for bit (1 % outlier channels x20, the plumbing config's
+    activations)."""
+    torch = pytest.importorskip("torch")
+    from oracle import float_torch as FT
+
+    x = OM.w8a8_linear_inputs(m=257, seed=7)[0]
+    codes, scale = FT.rot_q8(torch.from_numpy(x))
+    q, s = OR.rot_q8_1024(x)
+    assert np.array_equal(codes.numpy().astype(np.int8), q)
+    assert np.array_equal(scale.numpy().view(np.uint32), s.view(np.uint32))
+
+
+def test_float_torch_w8a8_linear_within_one_fp16_ulp():
+    """The plumbing config's W8A8 linear at full size (1025 x 1024 -> 3072) on the CPU against the oracle's
+    rot_q8_1024 + gemm_s8(EPI_BIAS_F16): identical codes, and the dequant rounds `acc * rs * cs + bias` after each
+    operation where the oracle (as the reference's compiler) fuses the last multiply-add: within one fp16 ulp."""
+    torch = pytest.importorskip("torch")
+    from oracle import float_torch as FT
+
+    x, qw, ws, b = OM.w8a8_linear_inputs()
+    got = FT.w8a8_linear(*(torch.from_numpy(a) for a in (x, qw, ws, b))).numpy().astype(np.float32)
+    a8, rs = OR.rot_q8_1024(x)
+    want = OG.gemm_s8(a8, qw, rs, ws, b, OG.EPI_BIAS_F16).astype(np.float32)
+    ulp = np.spacing(np.maximum(np.abs(got), np.abs(want)).astype(np.float16)).astype(np.float32)
+    assert (np.abs(got - want) <= ulp).all()
+
+
 # ---------------- planted mistakes: the checks above must catch them ----------------
 
 
