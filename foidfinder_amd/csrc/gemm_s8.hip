@@ -19,6 +19,8 @@
 //    slices (4 slots of K 64 when K % 128 != 0).
 //  * 4, gemm_s8_persist_kernel: variant 3's main loop on a persistent grid of one workgroup per CU whose ring runs on
 //    across tiles; the rows past the last whole 256-row tile follow in 32 x 32 blocks, split-K (large M).
+//  * 5, gemm_s8_wide_kernel<..., 128>: variant 3 on 256 x 128 tiles, each of its 8 waves a 64 x 64 sub-tile (narrow
+//    products at small M, where 256 x 256 tiles leave most CUs idle).
 //
 // Reference: foidfinder/backends/cuda/csrc/gemm.cuh:14-171 and kernels.cu:167-217.
 #include <type_traits>
@@ -528,9 +530,13 @@ __device__ __forceinline__ int wswz(int row, int chunk) {
     return rswz<RK>(row, chunk);
 }
 
-template <int EPI, int RK, int S>
+// BN_ = 256: each wave a 128 x 64 sub-tile (waves 2 x 4). BN_ = 128 (variant 5): each wave 64 x 64 (waves 4 x 2),
+// one fragment read per MFMA instead of 0.75 but twice the tiles, for narrow products whose 256 x 256 tiles leave
+// most CUs idle (PixAI's fc2 and proj at M = 5185, N = 1024: 84 tiles of 256 x 256, 168 of 256 x 128).
+template <int EPI, int RK, int S, int BN_ = 256>
 __global__ __launch_bounds__(512, 1) void gemm_s8_wide_kernel(const GemmArgs args) {
-  constexpr int BM = 256, BN = 256, WM = 128, WN = 64, MI = WM / 32, NI = WN / 32;
+  constexpr int BM = 256, BN = BN_, WM = BN == 256 ? 128 : 64, WN = 64, MI = WM / 32, NI = WN / 32;
+  constexpr int WCOLS = BN / WN;  // waves across the tile's columns
   constexpr int STAGE = (BM + BN) * RK;       // bytes per ring slot (64 KB or 32 KB)
   constexpr int LOADS = STAGE / (512 * 16);   // 16-byte loads per thread per slot (8 or 4)
   constexpr int A_BLOCKS = BM * RK / 1024;    // 1 KB blocks of A per slot; W blocks follow
@@ -540,7 +546,7 @@ __global__ __launch_bounds__(512, 1) void gemm_s8_wide_kernel(const GemmArgs arg
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 2, wn = wave & 3;
+  const int wm = wave / WCOLS, wn = wave % WCOLS;
   const int tiles_m = (args.M + BM - 1) / BM, tiles_n = (args.N + BN - 1) / BN;
   const int t = xcd_remap(blockIdx.x, gridDim.x);
   const int per_group = R_GROUP_M * tiles_n;
@@ -656,19 +662,19 @@ __global__ __launch_bounds__(512, 1) void gemm_s8_wide_kernel(const GemmArgs arg
   store_epilogue<EPI, NI, MI>(acc, m0 + wm * WM, n0 + wn * WN, lane, args, smem + wave * stage_bytes<EPI, NI>());
 }
 
-template <int RK, int S>
+template <int RK, int S, int BN = 256>
 static int launch_wide(const GemmArgs& a, int epi, hipStream_t st) {
   if (a.K % RK != 0) return fail(FF_EINVAL, "gemm_s8: K must be a multiple of the slice");
-  const int64_t tiles = static_cast<int64_t>((a.M + 255) / 256) * ((a.N + 255) / 256);
+  const int64_t tiles = static_cast<int64_t>((a.M + 255) / 256) * ((a.N + BN - 1) / BN);
   if (tiles > 0x7fffffff) return fail(FF_EINVAL, "gemm_s8: too many tiles");
   const dim3 grid(static_cast<unsigned>(tiles));
   switch (epi) {
-    case FF_EPI_QKV_ROPE: gemm_s8_wide_kernel<FF_EPI_QKV_ROPE, RK, S><<<grid, 512, 0, st>>>(a); break;
-    case FF_EPI_RESIDUAL: gemm_s8_wide_kernel<FF_EPI_RESIDUAL, RK, S><<<grid, 512, 0, st>>>(a); break;
-    case FF_EPI_GELU_F16: gemm_s8_wide_kernel<FF_EPI_GELU_F16, RK, S><<<grid, 512, 0, st>>>(a); break;
-    case FF_EPI_SWIGLU: gemm_s8_wide_kernel<FF_EPI_SWIGLU, RK, S><<<grid, 512, 0, st>>>(a); break;
-    case FF_EPI_BIAS_F16: gemm_s8_wide_kernel<FF_EPI_BIAS_F16, RK, S><<<grid, 512, 0, st>>>(a); break;
-    case FF_EPI_I32: gemm_s8_wide_kernel<FF_EPI_I32, RK, S><<<grid, 512, 0, st>>>(a); break;
+    case FF_EPI_QKV_ROPE: gemm_s8_wide_kernel<FF_EPI_QKV_ROPE, RK, S, BN><<<grid, 512, 0, st>>>(a); break;
+    case FF_EPI_RESIDUAL: gemm_s8_wide_kernel<FF_EPI_RESIDUAL, RK, S, BN><<<grid, 512, 0, st>>>(a); break;
+    case FF_EPI_GELU_F16: gemm_s8_wide_kernel<FF_EPI_GELU_F16, RK, S, BN><<<grid, 512, 0, st>>>(a); break;
+    case FF_EPI_SWIGLU: gemm_s8_wide_kernel<FF_EPI_SWIGLU, RK, S, BN><<<grid, 512, 0, st>>>(a); break;
+    case FF_EPI_BIAS_F16: gemm_s8_wide_kernel<FF_EPI_BIAS_F16, RK, S, BN><<<grid, 512, 0, st>>>(a); break;
+    case FF_EPI_I32: gemm_s8_wide_kernel<FF_EPI_I32, RK, S, BN><<<grid, 512, 0, st>>>(a); break;
     default: return fail(FF_EINVAL, "gemm_s8: bad epilogue");
   }
   return check_launch("gemm_s8");
@@ -1110,9 +1116,9 @@ static int launch_staged(const GemmArgs& a, int epi, hipStream_t st) {
 // 1: 128 x 128 register-staged; 2: 256 x 128 buffer->LDS ring (3 slots of K 64), two workgroups per CU;
 // 3: 256 x 256, 8 waves, one workgroup per CU (2 slots of K 128, or 4 slots of K 64 when K % 128 != 0);
 // 4: variant 3 as a persistent grid, the ring streaming across tiles (4 slots of K 64, not persistent, when
-// K % 128 != 0). These are the variants the engine's autotune picks at the served shapes (1 for small M, 2 and 3 for
-// mid-sized M and the narrower GEMMs, 4 for large M).
-constexpr int kVariants = 4;
+// K % 128 != 0); 5: variant 3 on 256 x 128 tiles of 64 x 64 per wave. These are the variants the engine's autotune
+// picks at the served shapes (1 and 5 for small M, 2, 3 and 5 for mid-sized M and the narrower GEMMs, 4 for large M).
+constexpr int kVariants = 5;
 
 }  // namespace ff
 
@@ -1170,6 +1176,7 @@ extern "C" int ff_gemm_s8(const int8_t* A, const int8_t* W, int64_t M, int64_t N
     case 2: return launch_ring<64, 3>(a, epi, st);
     case 3: return a.K % 128 == 0 ? launch_wide<128, 2>(a, epi, st) : launch_wide<64, 4>(a, epi, st);
     case 4: return a.K % 128 == 0 ? launch_persist(a, epi, st) : launch_wide<64, 4>(a, epi, st);
+    case 5: return a.K % 128 == 0 ? launch_wide<128, 2, 128>(a, epi, st) : launch_wide<64, 4, 128>(a, epi, st);
   }
   return fail(FF_EINVAL, "gemm_s8: bad variant");
 }
