@@ -147,7 +147,7 @@ def run_gemm(dev, a, w, rs, cs, bias, epi, variant, out=None, rope=None, q_scale
     return o.cpu().numpy()
 
 
-GEMM_VARIANTS = [1, 2, 3, 4, 5]  # ff_gemm_s8_variants()
+GEMM_VARIANTS = [1, 2, 3, 4, 5, 6]  # ff_gemm_s8_variants()
 PERSISTENT = 4  # the persistent 256 x 256 variant (with split-K blocks for the rows past the last whole tile)
 GEMM_SHAPES = [(1, 16, 64), (17, 48, 128), (300, 3072, 1024), (1025, 5632, 1024), (129, 1024, 2816), (257, 272, 192),
                (300, 1024, 2816)]
