@@ -764,19 +764,22 @@ __device__ __forceinline__ void tail_block(const GemmArgs& args, int m_first, in
 //
 // For products too small to fill the GPU with 256-wide tiles (EVA02-L at batch 1: fc2 at M = 1025, N = 1024 is 40
 // tiles of 256 x 128 for 256 CUs): the tail blocks' scheme at 64 x 64 over the whole matrix, 272 blocks there. Wave w
-// multiplies the 128-byte K chunks w, w + 8, ... of the block's 64 A rows and 64 W rows, each chunk staged in the
-// wave's own 16 KB of LDS by buffer->LDS loads (whole 128-byte rows per 8 lanes; rows past M or N read as zeros). The
-// eight int32 partial tiles are then summed exactly through LDS: each of four waves sums one 32 x 32 quadrant over
-// the eight and applies the epilogue to it. K % 128 == 0.
-constexpr int KS_CHUNK = 128 * 128;  // one staged chunk: 64 A rows + 64 W rows x 128 K bytes
+// multiplies the 64-byte K chunks w, w + 8, ... of the block's 64 A rows and 64 W rows, each chunk staged in the
+// wave's own 8 KB of LDS by buffer->LDS loads (rows past M or N read as zeros). The eight int32 partial tiles are then
+// summed exactly in two steps through the same 64 KB (waves 4-7 hand theirs to waves 0-3, then each of those four sums
+// one 32 x 32 quadrant over the four) and each of the four applies the epilogue to its quadrant. 64 KB of LDS and at
+// most 128 VGPRs let two workgroups share a CU, so all 272 blocks of that fc2 are resident at once.
+constexpr int KS_CHUNK = 128 * 64;     // one staged chunk: 64 A rows + 64 W rows x 64 K bytes
+constexpr int KS_PART = 64 * 64 * 4;   // one wave's 64 x 64 int32 partial tile
 
 template <int EPI>
-__global__ __launch_bounds__(512, 1) void gemm_s8_ksplit_kernel(const GemmArgs args) {
-  constexpr int SB = stage_bytes<EPI, 1>();
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[8 * KS_CHUNK + 4 * SB];
+__global__ __launch_bounds__(512, 2) void gemm_s8_ksplit_kernel(const GemmArgs args) {
+  static_assert(stage_bytes<EPI, 1>() <= KS_PART, "a quadrant's staging fits its wave's partial slot");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[8 * KS_CHUNK];  // chunks, then partials, then staging
+  static_assert(8 * KS_CHUNK == 4 * KS_PART, "four partial slots fill the chunk buffers");
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int fr = lane & 31, fk = lane >> 5;
-  const int M = args.M, N = args.N, K = args.K, nch = K / 128;
+  const int M = args.M, N = args.N, K = args.K, nch = K / 64;
   const int tiles_n = (N + 63) / 64;
   const int t = xcd_remap(blockIdx.x, gridDim.x);
   const int m0 = (t / tiles_n) * 64, n0 = (t % tiles_n) * 64;
@@ -784,61 +787,87 @@ __global__ __launch_bounds__(512, 1) void gemm_s8_ksplit_kernel(const GemmArgs a
   const int8_t* abase = args.A + static_cast<int64_t>(m0) * K;
   const int8_t* wbase = args.W + static_cast<int64_t>(n0) * K;
   uint8_t* mine = lds + wave * KS_CHUNK;
-  // Load p of a chunk fills LDS rows 8p .. 8p + 7 (rows 0-63: A, 64-127: W); lane l writes physical 16-byte slot l % 8
-  // of row 8p + l / 8, so it fetches the global chunk that the swizzle of wswz<128> puts there.
+  // Load p of a chunk fills LDS rows 16p .. 16p + 15 (rows 0-63: A, 64-127: W); lane l writes physical 16-byte slot
+  // l % 4 of row 16p + l / 4, so it fetches the global chunk that the swizzle of rswz<64> puts there.
   auto load_chunk = [&](int c) __attribute__((always_inline)) {
 #pragma unroll
-    for (int p = 0; p < 16; ++p) {
-      const int row = 8 * p + (lane >> 3), slot = lane & 7;
-      const uint32_t voff = static_cast<uint32_t>((row & 63) * K + c * 128 + ((slot ^ ((row >> 1) & 7)) << 4));
-      if (p < 8)
+    for (int p = 0; p < 8; ++p) {
+      const int row = 16 * p + (lane >> 2), slot = lane & 3;
+      const uint32_t voff = static_cast<uint32_t>((row & 63) * K + c * 64 + ((slot ^ ((row >> 2) & 3)) << 4));
+      if (p < 4)
         buffer_to_lds(abase, a_bytes, mine + p * 1024, voff);
       else
         buffer_to_lds(wbase, w_bytes, mine + p * 1024, voff);
     }
   };
   int16_t_v acc[2][2] = {};
+  if (wave < nch) load_chunk(wave);
   for (int c = wave; c < nch; c += 8) {
-    load_chunk(c);
+    // the chunk's fragments into registers, then the buffer takes the wave's next chunk while these multiply
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    int4_t xw[2][2], ya[2][2];  // [k-step][block]
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      int4_t xw[2], ya[2];
+    for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) xw[i] = *reinterpret_cast<const int4_t*>(mine + wswz<128>(64 + 32 * i + fr, 2 * kk + fk));
+      for (int i = 0; i < 2; ++i)
+        xw[kk][i] = *reinterpret_cast<const int4_t*>(mine + rswz<64>(64 + 32 * i + fr, 2 * kk + fk));
 #pragma unroll
-      for (int j = 0; j < 2; ++j) ya[j] = *reinterpret_cast<const int4_t*>(mine + wswz<128>(32 * j + fr, 2 * kk + fk));
+      for (int j = 0; j < 2; ++j) ya[kk][j] = *reinterpret_cast<const int4_t*>(mine + rswz<64>(32 * j + fr, 2 * kk + fk));
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (c + 8 < nch) load_chunk(c + 8);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int i = 0; i < 2; ++i) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xw[i], ya[j], acc[i][j], 0, 0, 0);
-    }
-    // the next chunk's loads overwrite these rows: every read above has completed
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        for (int i = 0; i < 2; ++i)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xw[kk][i], ya[kk][j], acc[i][j], 0, 0, 0);
   }
-  // the partial tile into the wave's own buffer (its chunk reads are done): quadrant (i, j) at 4 KB (2 i + j),
-  // 16-byte chunk q of lane l at 1 KB q + 16 l
+  // A partial tile in slot s: quadrant (i, j) at 4 KB (2 i + j), 16-byte chunk q of lane l at 1 KB q + 16 l.
+  auto put = [&](int s) __attribute__((always_inline)) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<int4_t*>(mine + (2 * i + j) * 4096 + q * 1024 + lane * 16) =
-            int4_t{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<int4_t*>(lds + s * KS_PART + (2 * i + j) * 4096 + q * 1024 + lane * 16) =
+              int4_t{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+  };
+  __syncthreads();  // every wave is done with its chunk buffer
+  if (wave >= 4) put(wave - 4);
   __syncthreads();
-  if (wave >= 4) return;
-  const int qi = wave >> 1, qj = wave & 1;  // this wave's quadrant: column block qi, row block qj
+  if (wave < 4) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int4_t v = *reinterpret_cast<const int4_t*>(lds + wave * KS_PART + (2 * i + j) * 4096 + q * 1024 + lane * 16);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += v[e];
+        }
+  }
+  __syncthreads();  // waves 0-3 have read the slots they now overwrite
+  if (wave < 4) put(wave);
+  __syncthreads();
+  const int qi = (wave >> 1) & 1, qj = wave & 1;  // waves 0-3: the quadrant, column block qi, row block qj
   int16_t_v sum[1][1] = {};
+  if (wave < 4) {
 #pragma unroll
-  for (int w = 0; w < 8; ++w)
+    for (int s = 0; s < 4; ++s)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int4_t v = *reinterpret_cast<const int4_t*>(lds + w * KS_CHUNK + (2 * qi + qj) * 4096 + q * 1024 + lane * 16);
+      for (int q = 0; q < 4; ++q) {
+        const int4_t v = *reinterpret_cast<const int4_t*>(lds + s * KS_PART + (2 * qi + qj) * 4096 + q * 1024 + lane * 16);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) sum[0][0][4 * q + e] += v[e];
-    }
-  store_epilogue<EPI, 1, 1>(sum, m0 + 32 * qj, n0 + 32 * qi, lane, args, lds + 8 * KS_CHUNK + wave * SB);
+        for (int e = 0; e < 4; ++e) sum[0][0][4 * q + e] += v[e];
+      }
+  }
+  __syncthreads();  // every quadrant is read: the slots become the epilogue's staging areas
+  if (wave >= 4) return;
+  store_epilogue<EPI, 1, 1>(sum, m0 + 32 * qj, n0 + 32 * qi, lane, args, lds + wave * KS_PART);
 }
 
 static int launch_ksplit(const GemmArgs& a, int epi, hipStream_t st) {
@@ -1215,8 +1244,7 @@ static int launch_staged(const GemmArgs& a, int epi, hipStream_t st) {
 // 1: 128 x 128 register-staged; 2: 256 x 128 buffer->LDS ring (3 slots of K 64), two workgroups per CU;
 // 3: 256 x 256, 8 waves, one workgroup per CU (2 slots of K 128, or 4 slots of K 64 when K % 128 != 0);
 // 4: variant 3 as a persistent grid, the ring streaming across tiles (4 slots of K 64, not persistent, when
-// K % 128 != 0); 5: variant 3 on 256 x 128 tiles of 64 x 64 per wave; 6: 64 x 64 blocks with K split over 8 waves
-// (variant 1 when K % 128 != 0). These are the variants the engine's autotune picks at the served shapes (1, 5 and 6
+// K % 128 != 0); 5: variant 3 on 256 x 128 tiles of 64 x 64 per wave; 6: 64 x 64 blocks with K split over 8 waves. These are the variants the engine's autotune picks at the served shapes (1, 5 and 6
 // for small M, 2, 3 and 5 for mid-sized M and the narrower GEMMs, 4 for large M).
 constexpr int kVariants = 6;
 
@@ -1277,7 +1305,7 @@ extern "C" int ff_gemm_s8(const int8_t* A, const int8_t* W, int64_t M, int64_t N
     case 3: return a.K % 128 == 0 ? launch_wide<128, 2>(a, epi, st) : launch_wide<64, 4>(a, epi, st);
     case 4: return a.K % 128 == 0 ? launch_persist(a, epi, st) : launch_wide<64, 4>(a, epi, st);
     case 5: return a.K % 128 == 0 ? launch_wide<128, 2, 128>(a, epi, st) : launch_wide<64, 4, 128>(a, epi, st);
-    case 6: return a.K % 128 == 0 ? launch_ksplit(a, epi, st) : launch_staged<128, 128>(a, epi, st);
+    case 6: return launch_ksplit(a, epi, st);
   }
   return fail(FF_EINVAL, "gemm_s8: bad variant");
 }
