@@ -21,7 +21,7 @@
 //    across tiles; the rows past the last whole 256-row tile follow in 32 x 32 blocks, split-K (large M).
 //  * 5, gemm_s8_wide_kernel<..., 128>: variant 3 on 256 x 128 tiles, each of its 8 waves a 64 x 64 sub-tile (narrow
 //    products at small M, where 256 x 256 tiles leave most CUs idle).
-//  * 6, gemm_s8_ksplit_kernel: 64 x 64 blocks, each over all of K split across its 8 waves and summed through LDS
+//  * 6, gemm_s8_ksplit_kernel: 64 x 64 blocks, each over all of K split across its 4 waves and summed through LDS
 //    (small M, where even 256 x 128 tiles leave most CUs idle).
 //
 // Reference: foidfinder/backends/cuda/csrc/gemm.cuh:14-171 and kernels.cu:167-217.
@@ -760,23 +760,28 @@ __device__ __forceinline__ void tail_block(const GemmArgs& args, int m_first, in
   store_epilogue<EPI, 1, 1>(acc, m0, n0, lane, args, lds);
 }
 
-// ---------------- variant 6: 64 x 64 blocks, K split over the workgroup's 8 waves ----------------
+// ---------------- variant 6: 64 x 64 blocks, K split over the workgroup's 4 waves ----------------
 //
 // For products too small to fill the GPU with 256-wide tiles (EVA02-L at batch 1: fc2 at M = 1025, N = 1024 is 40
 // tiles of 256 x 128 for 256 CUs): the tail blocks' scheme at 64 x 64 over the whole matrix, 272 blocks there. Wave w
-// multiplies the 64-byte K chunks w, w + 8, ... of the block's 64 A rows and 64 W rows, each chunk staged in the
-// wave's own 8 KB of LDS by buffer->LDS loads (rows past M or N read as zeros). The eight int32 partial tiles are then
-// summed exactly in two steps through the same 64 KB (waves 4-7 hand theirs to waves 0-3, then each of those four sums
-// one 32 x 32 quadrant over the four) and each of the four applies the epilogue to its quadrant. 64 KB of LDS and at
-// most 128 VGPRs let two workgroups share a CU, so all 272 blocks of that fc2 are resident at once.
+// of the block's WV waves multiplies the 64-byte K chunks w, w + WV, ... of its 64 A rows and 64 W rows, each chunk
+// staged in the wave's own 8 KB of LDS by buffer->LDS loads (rows past M or N read as zeros; the chunk's fragments go
+// to registers before the wave's next chunk loads into the buffer). The int32 partial tiles are then summed exactly in
+// two steps through the same LDS (the upper half of the waves hands theirs to the lower half, then each of waves 0-3
+// sums one 32 x 32 quadrant over those) and each of waves 0-3 applies the epilogue to its quadrant. With WV = 4 a
+// block takes 32 KB and at most 128 VGPRs, so four share a CU and 1024 are resident (EVA02-L's qkv at batch 1 is 816
+// blocks). Measured at batch 1 (fc2 / proj / qkv): 11.1 / 6.5 / 11.2 us; the same kernel with 8 waves per block (64
+// KB, two per CU) ran 12.8 / 7.8 / 13.8.
 constexpr int KS_CHUNK = 128 * 64;     // one staged chunk: 64 A rows + 64 W rows x 64 K bytes
 constexpr int KS_PART = 64 * 64 * 4;   // one wave's 64 x 64 int32 partial tile
 
 template <int EPI>
-__global__ __launch_bounds__(512, 2) void gemm_s8_ksplit_kernel(const GemmArgs args) {
-  static_assert(stage_bytes<EPI, 1>() <= KS_PART, "a quadrant's staging fits its wave's partial slot");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[8 * KS_CHUNK];  // chunks, then partials, then staging
-  static_assert(8 * KS_CHUNK == 4 * KS_PART, "four partial slots fill the chunk buffers");
+__global__ __launch_bounds__(256, 4) void gemm_s8_ksplit_kernel(const GemmArgs args) {
+  constexpr int WV = 4;          // waves per block
+  constexpr int SLOTS = WV / 2;  // partial slots in the chunk buffers
+  static_assert(stage_bytes<EPI, 1>() <= KS_CHUNK, "a quadrant's staging fits its wave's chunk buffer");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[WV * KS_CHUNK];  // chunks, then partials, then staging
+  static_assert(WV * KS_CHUNK == SLOTS * KS_PART, "the partial slots fill the chunk buffers");
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int fr = lane & 31, fk = lane >> 5;
   const int M = args.M, N = args.N, K = args.K, nch = K / 64;
@@ -802,7 +807,7 @@ __global__ __launch_bounds__(512, 2) void gemm_s8_ksplit_kernel(const GemmArgs a
   };
   int16_t_v acc[2][2] = {};
   if (wave < nch) load_chunk(wave);
-  for (int c = wave; c < nch; c += 8) {
+  for (int c = wave; c < nch; c += WV) {
     // the chunk's fragments into registers, then the buffer takes the wave's next chunk while these multiply
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     int4_t xw[2][2], ya[2][2];  // [k-step][block]
@@ -815,7 +820,7 @@ __global__ __launch_bounds__(512, 2) void gemm_s8_ksplit_kernel(const GemmArgs a
       for (int j = 0; j < 2; ++j) ya[kk][j] = *reinterpret_cast<const int4_t*>(mine + rswz<64>(32 * j + fr, 2 * kk + fk));
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if (c + 8 < nch) load_chunk(c + 8);
+    if (c + WV < nch) load_chunk(c + WV);
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -836,9 +841,10 @@ __global__ __launch_bounds__(512, 2) void gemm_s8_ksplit_kernel(const GemmArgs a
               int4_t{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
   };
   __syncthreads();  // every wave is done with its chunk buffer
-  if (wave >= 4) put(wave - 4);
+  // step 1: the upper half of the waves hands its partials to the lower half
+  if (wave >= SLOTS) put(wave - SLOTS);
   __syncthreads();
-  if (wave < 4) {
+  if (wave < SLOTS) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -850,14 +856,15 @@ __global__ __launch_bounds__(512, 2) void gemm_s8_ksplit_kernel(const GemmArgs a
           for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += v[e];
         }
   }
-  __syncthreads();  // waves 0-3 have read the slots they now overwrite
-  if (wave < 4) put(wave);
+  __syncthreads();  // the lower half has read the slots it now overwrites
+  // step 2: the lower half's sums into the slots; waves 0-3 each sum one quadrant over them
+  if (wave < SLOTS) put(wave);
   __syncthreads();
   const int qi = (wave >> 1) & 1, qj = wave & 1;  // waves 0-3: the quadrant, column block qi, row block qj
   int16_t_v sum[1][1] = {};
   if (wave < 4) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+    for (int s = 0; s < SLOTS; ++s)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int4_t v = *reinterpret_cast<const int4_t*>(lds + s * KS_PART + (2 * qi + qj) * 4096 + q * 1024 + lane * 16);
@@ -865,9 +872,9 @@ __global__ __launch_bounds__(512, 2) void gemm_s8_ksplit_kernel(const GemmArgs a
         for (int e = 0; e < 4; ++e) sum[0][0][4 * q + e] += v[e];
       }
   }
-  __syncthreads();  // every quadrant is read: the slots become the epilogue's staging areas
+  __syncthreads();  // every quadrant is read: the chunk buffers become the epilogue's staging areas
   if (wave >= 4) return;
-  store_epilogue<EPI, 1, 1>(sum, m0 + 32 * qj, n0 + 32 * qi, lane, args, lds + wave * KS_PART);
+  store_epilogue<EPI, 1, 1>(sum, m0 + 32 * qj, n0 + 32 * qi, lane, args, lds + wave * KS_CHUNK);
 }
 
 static int launch_ksplit(const GemmArgs& a, int epi, hipStream_t st) {
@@ -875,12 +882,12 @@ static int launch_ksplit(const GemmArgs& a, int epi, hipStream_t st) {
   if (blocks > 0x7fffffff) return fail(FF_EINVAL, "gemm_s8: too many tiles");
   const dim3 grid(static_cast<unsigned>(blocks));
   switch (epi) {
-    case FF_EPI_QKV_ROPE: gemm_s8_ksplit_kernel<FF_EPI_QKV_ROPE><<<grid, 512, 0, st>>>(a); break;
-    case FF_EPI_RESIDUAL: gemm_s8_ksplit_kernel<FF_EPI_RESIDUAL><<<grid, 512, 0, st>>>(a); break;
-    case FF_EPI_GELU_F16: gemm_s8_ksplit_kernel<FF_EPI_GELU_F16><<<grid, 512, 0, st>>>(a); break;
-    case FF_EPI_SWIGLU: gemm_s8_ksplit_kernel<FF_EPI_SWIGLU><<<grid, 512, 0, st>>>(a); break;
-    case FF_EPI_BIAS_F16: gemm_s8_ksplit_kernel<FF_EPI_BIAS_F16><<<grid, 512, 0, st>>>(a); break;
-    case FF_EPI_I32: gemm_s8_ksplit_kernel<FF_EPI_I32><<<grid, 512, 0, st>>>(a); break;
+    case FF_EPI_QKV_ROPE: gemm_s8_ksplit_kernel<FF_EPI_QKV_ROPE><<<grid, 256, 0, st>>>(a); break;
+    case FF_EPI_RESIDUAL: gemm_s8_ksplit_kernel<FF_EPI_RESIDUAL><<<grid, 256, 0, st>>>(a); break;
+    case FF_EPI_GELU_F16: gemm_s8_ksplit_kernel<FF_EPI_GELU_F16><<<grid, 256, 0, st>>>(a); break;
+    case FF_EPI_SWIGLU: gemm_s8_ksplit_kernel<FF_EPI_SWIGLU><<<grid, 256, 0, st>>>(a); break;
+    case FF_EPI_BIAS_F16: gemm_s8_ksplit_kernel<FF_EPI_BIAS_F16><<<grid, 256, 0, st>>>(a); break;
+    case FF_EPI_I32: gemm_s8_ksplit_kernel<FF_EPI_I32><<<grid, 256, 0, st>>>(a); break;
     default: return fail(FF_EINVAL, "gemm_s8: bad epilogue");
   }
   return check_launch("gemm_s8");
@@ -1244,7 +1251,7 @@ static int launch_staged(const GemmArgs& a, int epi, hipStream_t st) {
 // 1: 128 x 128 register-staged; 2: 256 x 128 buffer->LDS ring (3 slots of K 64), two workgroups per CU;
 // 3: 256 x 256, 8 waves, one workgroup per CU (2 slots of K 128, or 4 slots of K 64 when K % 128 != 0);
 // 4: variant 3 as a persistent grid, the ring streaming across tiles (4 slots of K 64, not persistent, when
-// K % 128 != 0); 5: variant 3 on 256 x 128 tiles of 64 x 64 per wave; 6: 64 x 64 blocks with K split over 8 waves. These are the variants the engine's autotune picks at the served shapes (1, 5 and 6
+// K % 128 != 0); 5: variant 3 on 256 x 128 tiles of 64 x 64 per wave; 6: 64 x 64 blocks with K split over 4 waves. These are the variants the engine's autotune picks at the served shapes (1, 5 and 6
 // for small M, 2, 3 and 5 for mid-sized M and the narrower GEMMs, 4 for large M).
 constexpr int kVariants = 6;
 
