@@ -19,8 +19,8 @@
 //    slices (4 slots of K 64 when K % 128 != 0).
 //  * 4, gemm_s8_persist_kernel: variant 3's main loop on a persistent grid of one workgroup per CU whose ring runs on
 //    across tiles; the rows past the last whole 256-row tile follow in 32 x 32 blocks, split-K (large M).
-//  * 5, gemm_s8_wide_kernel<..., 128>: variant 3 on 256 x 128 tiles, each of its 8 waves a 64 x 64 sub-tile (narrow
-//    products at small M, where 256 x 256 tiles leave most CUs idle).
+//  * 5, gemm_s8_wide_kernel<..., 128>: variant 3 on 256 x 128 tiles, each of its 8 waves a 64 x 64 sub-tile, with a
+//    3-slot ring (narrow products at small M, where 256 x 256 tiles leave most CUs idle).
 //  * 6, gemm_s8_ksplit_kernel: 64 x 64 blocks, each over all of K split across its 4 waves and summed through LDS
 //    (small M, where even 256 x 128 tiles leave most CUs idle).
 //
@@ -534,7 +534,9 @@ __device__ __forceinline__ int wswz(int row, int chunk) {
 
 // BN_ = 256: each wave a 128 x 64 sub-tile (waves 2 x 4). BN_ = 128 (variant 5): each wave 64 x 64 (waves 4 x 2),
 // one fragment read per MFMA instead of 0.75 but twice the tiles, for narrow products whose 256 x 256 tiles leave
-// most CUs idle (PixAI's fc2 and proj at M = 5185, N = 1024: 84 tiles of 256 x 256, 168 of 256 x 128).
+// most CUs idle (PixAI's fc2 and proj at M = 5185, N = 1024: 84 tiles of 256 x 256, 168 of 256 x 128). Its 48 KB
+// slots leave room for a third (144 KB), so the next two slices load while one computes: at small M the weights
+// arrive cold from HBM, and one slice of prefetch does not cover that latency.
 template <int EPI, int RK, int S, int BN_ = 256>
 __global__ __launch_bounds__(512, 1) void gemm_s8_wide_kernel(const GemmArgs args) {
   constexpr int BM = 256, BN = BN_, WM = BN == 256 ? 128 : 64, WN = 64, MI = WM / 32, NI = WN / 32;
@@ -1251,7 +1253,8 @@ static int launch_staged(const GemmArgs& a, int epi, hipStream_t st) {
 // 1: 128 x 128 register-staged; 2: 256 x 128 buffer->LDS ring (3 slots of K 64), two workgroups per CU;
 // 3: 256 x 256, 8 waves, one workgroup per CU (2 slots of K 128, or 4 slots of K 64 when K % 128 != 0);
 // 4: variant 3 as a persistent grid, the ring streaming across tiles (4 slots of K 64, not persistent, when
-// K % 128 != 0); 5: variant 3 on 256 x 128 tiles of 64 x 64 per wave; 6: 64 x 64 blocks with K split over 4 waves. These are the variants the engine's autotune picks at the served shapes (1, 5 and 6
+// K % 128 != 0); 5: variant 3 on 256 x 128 tiles of 64 x 64 per wave, 3 slots of K 128; 6: 64 x 64 blocks with K
+// split over 4 waves. These are the variants the engine's autotune picks at the served shapes (1, 5 and 6
 // for small M, 2, 3 and 5 for mid-sized M and the narrower GEMMs, 4 for large M).
 constexpr int kVariants = 6;
 
@@ -1311,7 +1314,7 @@ extern "C" int ff_gemm_s8(const int8_t* A, const int8_t* W, int64_t M, int64_t N
     case 2: return launch_ring<64, 3>(a, epi, st);
     case 3: return a.K % 128 == 0 ? launch_wide<128, 2>(a, epi, st) : launch_wide<64, 4>(a, epi, st);
     case 4: return a.K % 128 == 0 ? launch_persist(a, epi, st) : launch_wide<64, 4>(a, epi, st);
-    case 5: return a.K % 128 == 0 ? launch_wide<128, 2, 128>(a, epi, st) : launch_wide<64, 4, 128>(a, epi, st);
+    case 5: return a.K % 128 == 0 ? launch_wide<128, 3, 128>(a, epi, st) : launch_wide<64, 4, 128>(a, epi, st);
     case 6: return launch_ksplit(a, epi, st);
   }
   return fail(FF_EINVAL, "gemm_s8: bad variant");
