@@ -241,8 +241,10 @@ class Int8Engine:
         """Pick the fastest GEMM tile variant per GEMM for this batch size (engine.py:108-135). The activation
         operands are codes distributed like the rotations' output (a rotated row is close to Gaussian, and its
         absmax sits near 3.3 standard deviations, so codes ~ N(0, 38^2)), not zeros or uniform codes: MFMA power and
-        so the clock depend on the data. Each variant is timed in three interleaved rounds and keeps its best round,
-        so a momentary clock dip does not decide the pick."""
+        so the clock depend on the data. Each variant's launches are captured in a HIP graph and replayed, so the
+        host's launch cost (which exceeds a short GEMM's run time at small batches, and more so under a profiler)
+        does not mask the differences; each is timed in three interleaved rounds and keeps its best round, so a
+        momentary clock dip does not decide the pick."""
         g = torch.Generator(device=buf["a8"].device).manual_seed(0)
         for name in ("a8", "h8"):
             t = buf[name]
@@ -253,18 +255,25 @@ class Int8Engine:
         buf["o16"].zero_()
         n = lib().ff_gemm_s8_variants()
         for name, fn in self._gemm_jobs(buf).items():
-            times = {v: float("inf") for v in range(1, n + 1)}
-            for _ in range(3):
-                for v in times:
-                    for _ in range(2):
-                        fn(v)
-                    start, end = torch.cuda.Event(True), torch.cuda.Event(True)
-                    start.record()
+            graphs = {}
+            for v in range(1, n + 1):
+                fn(v)  # eager first: a variant that rejects the shape raises here, outside any capture
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
                     for _ in range(5):
                         fn(v)
+                graphs[v] = graph
+            times = {v: float("inf") for v in graphs}
+            for _ in range(3):
+                for v, graph in graphs.items():
+                    graph.replay()
+                    start, end = torch.cuda.Event(True), torch.cuda.Event(True)
+                    start.record()
+                    graph.replay()
                     end.record()
                     torch.cuda.synchronize()
                     times[v] = min(times[v], start.elapsed_time(end))
+            del graphs
             self.variants[(name, B)] = min(times, key=times.get)
 
     def eager(self, images: torch.Tensor, trace: dict | None = None) -> torch.Tensor:
