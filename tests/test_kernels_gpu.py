@@ -169,6 +169,35 @@ def test_gemm_s8_int32_bit_exact(dev, rng, M, N, K, variant):
     assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[:4].tolist()}: {got[tuple(bad[0])]} vs {want[tuple(bad[0])]}"
 
 
+def _random_gemm_shapes(n: int, seed: int = 7) -> list[tuple[int, int, int]]:
+    """Seeded shapes off every tile grid: M anywhere in 1..600 (with the 64-, 128- and 256-row tile edges), N any
+    multiple of 16 up to 512, K any multiple of 64 up to 1280 (odd multiples take the K-64 rings)."""
+    r = np.random.default_rng(seed)
+    edges = [63, 64, 65, 127, 129, 255, 256, 257, 511, 513]
+    return [(int(edges[i] if i < len(edges) and i % 2 == 0 else r.integers(1, 601)), 16 * int(r.integers(1, 33)),
+             64 * int(r.integers(1, 21))) for i in range(n)]
+
+
+RANDOM_GEMM_SHAPES = _random_gemm_shapes(8)
+_random_gemm_cache: dict = {}
+
+
+@pytest.mark.parametrize("variant", GEMM_VARIANTS)
+@pytest.mark.parametrize("shape", range(len(RANDOM_GEMM_SHAPES)))
+def test_gemm_s8_random_shapes_int32_bit_exact(dev, shape, variant):
+    """Every tile variant on the same seeded shapes (inputs drawn once per shape, the oracle product computed once)."""
+    M, N, K = RANDOM_GEMM_SHAPES[shape]
+    if shape not in _random_gemm_cache:
+        a, w, *_ = gemm_inputs(np.random.default_rng(1000 + shape), M, N, K)
+        _random_gemm_cache[shape] = (a, w, OG.gemm_s8_i32(a, w))
+    a, w, want = _random_gemm_cache[shape]
+    ones = np.ones(M, np.float32)
+    got = run_gemm(dev, a, w, ones, np.ones(N, np.float32), np.zeros(N, np.float32), OG.EPI_I32, variant)
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, (f"M={M} N={N} K={K} variant {variant}: {len(bad)} mismatches, first at "
+                           f"{bad[:4].tolist()}")
+
+
 @pytest.mark.parametrize("variant", GEMM_VARIANTS)
 @pytest.mark.parametrize("epi", [OG.EPI_BIAS_F16, OG.EPI_RESIDUAL, OG.EPI_QKV_ROPE, OG.EPI_SWIGLU])
 def test_gemm_s8_epilogue_bit_exact(dev, rng, epi, variant):
