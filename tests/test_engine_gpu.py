@@ -173,6 +173,29 @@ def test_full_size_batch_32_is_permutation_equivariant(dev):
     assert torch.equal(shuffled, full[perm]), "permuting the batch does not permute the logits"
 
 
+def test_full_size_logits_do_not_depend_on_gemm_variants(dev):
+    """EVA02-L/14-448 at batch 1 (1025 tokens, 24 blocks): every GEMM tile variant is bit-exact in int32 and
+    applies the same epilogue arithmetic, so the logits are bit-identical whichever variants the autotune picks.
+    Checked with the autotune's own picks (graph replay) against each variant forced on all four GEMMs (eager)."""
+    from foidfinder_amd import kernels as K
+    from foidfinder_amd.engine import GEMMS, Eva02Config, Eva02Int8
+
+    cfg = Eva02Config()
+    _, state = raw_and_converted(cfg, seed=5)
+    eng = Eva02Int8(state, cfg, device=dev)
+    images = torch.from_numpy(OM.synthetic_images(1, cfg.img_size, seed=10)).to(dev)
+    tuned = eng(images).clone()
+    torch.cuda.synchronize()
+    assert torch.isfinite(tuned).all()
+    picks = {name: eng.variants[(name, 1)] for name in GEMMS}
+    for v in range(1, K.lib().ff_gemm_s8_variants() + 1):
+        for name in GEMMS:
+            eng.variants[(name, 1)] = v
+        forced = eng.eager(images)
+        assert torch.equal(forced, tuned), (f"variant {v} on every GEMM differs from the autotuned picks {picks}: "
+                                            f"{(forced - tuned).abs().max().item()}")
+
+
 # The stated end-to-end bars at the benchmark's model (EVA02-L/14-448, 24 blocks, 1025 tokens), without teacher
 # forcing, against each reference: max |dp| and max |dlogit| over all tags and images at most E2E_REL_MAX times the
 # int8 noise (the same maxima of the int8 oracle against the float forward, on the same images), mean |dp| at most
