@@ -1308,7 +1308,9 @@ extern "C" int ff_gemm_s8(const int8_t* A, const int8_t* W, int64_t M, int64_t N
   a.rope_len = static_cast<int>(rope_len);
   a.q_scale = q_scale;
   hipStream_t st = as_stream(stream);
-  if (variant == 0) variant = M < 2048 ? 1 : (M < 16384 ? 2 : 4);
+  // The default follows the autotune's usual picks: K-split 64 x 64 blocks while they fill the GPU, 256 x 256 tiles
+  // for mid-size M, the persistent grid from a few tiles per CU on.
+  if (variant == 0) variant = M < 4096 ? 6 : (M < 16384 ? 3 : 4);
   switch (variant) {
     case 1: return launch_staged<128, 128>(a, epi, st);
     case 2: return launch_ring<64, 3>(a, epi, st);

@@ -59,7 +59,7 @@ int ff_rot_q8_h128(const void* x, int64_t T, int64_t C, int64_t c_real, const fl
  * 1 = 128x128 register-staged, 2 = 256x128 buffer->LDS ring (two workgroups per CU), 3 = 256x256 with 8 waves,
  * 4 = variant 3 on a persistent grid (the rows past the last whole 256-row tile as split-K blocks in the same
  * launch), 5 = variant 3 on 256x128 tiles (narrow products at small M), 6 = 64x64 blocks with K split over
- * 4 waves (small M); 0 = a default by M (1 below 2048 rows, 2 below 16384, else 4). All give identical
+ * 4 waves (small M); 0 = a default by M (6 below 4096 rows, 3 below 16384, else 4). All give identical
  * results.
  * Replaces op `gemm_s8(A, W, row_scale, col_scale, bias, out!, epi, stages, rope_cos?, rope_sin?, q_scale)`,
  * foidfinder/backends/cuda/csrc/kernels.cu:187-217, whose `stages` is the same kind of autotuned knob. */
