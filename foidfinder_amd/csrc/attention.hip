@@ -410,10 +410,21 @@ __global__ __launch_bounds__(64 * WAVES, 4) void attention_kernel(const half_t* 
   // K tile of ring slot st at smem + st*TILE, V tile at smem + (STAGES + st)*TILE
   __shared__ __attribute__((aligned(1024))) half_t smem[2 * STAGES * TILE];
   // 1-D grid over (sequence, head, query block), query block fastest, remapped so that all query blocks of one
-  // (sequence, head) run on one XCD and read its K and V through one L2.
+  // (sequence, head) run on one XCD and read its K and V through one L2. When each XCD's share is whole (sequence,
+  // head) groups, its partial last query blocks (L = 1025: a single query, a quarter of a block's time) are ordered
+  // after its whole blocks, so they fill the end of the grid instead of leaving it to a last round of whole blocks
+  // (measured at 32 x 16 x 1025: 169.4 vs 172.6 us; at 16 x 16 x 1025: 87.8 vs 91.0; the same results).
   const int nq = (L + bq - 1) / bq;
   const int t = xcd_remap(blockIdx.x, gridDim.x);
-  const int qb = t % nq, h = (t / nq) % H, seq = t / (nq * H);
+  int qb = t % nq, h = (t / nq) % H, seq = t / (nq * H);
+  const int per = static_cast<int>(gridDim.x) >> 3;  // blocks per XCD
+  if ((gridDim.x & 7) == 0 && per % nq == 0 && L % bq != 0 && nq > 1) {
+    const int x = t / per, k = t % per, whole = per / nq * (nq - 1);
+    const int pair = x * (per / nq) + (k < whole ? k / (nq - 1) : k - whole);
+    qb = k < whole ? k % (nq - 1) : nq - 1;
+    h = pair % H;
+    seq = pair / H;
+  }
   const int q_first = qb * bq;
   const int units = min(bq / QW, (L - q_first + QW - 1) / QW);  // 32-query units of this block
   if (units == 1)
