@@ -17,7 +17,8 @@
 // tile is processed in two 32-key halves (S, softmax, PV per half). At head_dim 64 the softmax, not the MFMA, bounds
 // the loop, so its common path is one exp2, half a convert and half a packed add per score:
 //  * every S^T accumulator starts at -m_ref (the query's reference maximum, kept fp16-representable): a register
-//    block holding -m_ref is the C operand of each half's first product; the first tile sets m_ref to its maximum;
+//    block holding -m_ref is the C operand of each half's first product; the first tile's first key half sets m_ref
+//    to its maximum;
 //  * p = v_exp_f32 (exp2), converted in pairs to fp16 for the PV product; each lane sums those fp16 p (the weights the
 //    PV product applies) by a pairwise tree of v_pk_add_f16 (7 packed adds per 16 p) and one exact fp32 add of the
 //    last pair, and the half sums accumulate in fp32. The tree rounds to fp16 at each level (relative error at most
@@ -316,17 +317,13 @@ __device__ __forceinline__ void attention_block(const half_t* __restrict__ qkv, 
       va[dt] = (STAGES + st) * TILE + voff[dt];
       asm volatile("" : "+v"(va[dt]));
     }
-    // Each half's p are checked (all lane sums <= SUM_LIMIT) before its PV product; the wave's first tile sets m_ref
-    // from its maximum first.
+    // Each half's p are checked (all lane sums <= SUM_LIMIT) before its PV product. The wave's first tile sets m_ref
+    // from the maximum of its first half (one extra S product per wave; the second half, like every later one, takes
+    // the rescue path if its scores rise well above it). From both halves' maximum it cost a second extra product and
+    // ran ~0.7 % slower.
     if (tile == first_tile) {
       qk(0, lastc);
-      if constexpr (SPLIT) {
-        set_mref(half_max());
-      } else {
-        const float m0 = half_max();
-        qk(1, lastc);
-        set_mref(fmaxf(m0, half_max()));
-      }
+      set_mref(half_max());
     }
     qk(0, lastc);
     soft(0);
